@@ -1,0 +1,262 @@
+#!/usr/bin/env python3
+"""Headline benchmark of the gfx950 stream and GEMM kernels on one MI355X.
+
+One step is one launch of the stream triad a = b + 3*c over 2^28 fp32
+elements per array (3 GiB of algorithmic traffic), through the C ABI of
+libmi355bench.so on torch's current stream, with the inputs already resident
+in HBM. The printed JSON line carries:
+
+  value / ms_per_step  whole-job triad GB/s and the wall-clock time per step
+                       (K launches between two device synchronisations);
+  roofline             the triad kernel's algorithmic GB/s from HIP events
+                       recorded on the launch stream, against 8000 GB/s;
+                       `traffic` is the HBM bytes per launch from the committed
+                       rocprofv3 FETCH_SIZE/WRITE_SIZE summary, when present;
+  gemm                 bf16 and fp8 e4m3 GEMM TFLOPS and MFU at 8192^3
+                       (event-timed, same library), with a sampled parity check;
+  cpu_baseline         the reference torch op (torch.add(b, c, alpha=3.0,
+                       out=a)) on CPU tensors on this host's cores, timed over a
+                       bounded sample of the same workload.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-gemm]
+                       [--cpu-seconds S]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+from pathlib import Path
+import sys
+import time
+
+ROOT = Path(__file__).resolve().parent
+if str(ROOT) not in sys.path:
+    sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBPS = 8000.0
+MFMA_PEAK_TFLOPS = {"bfloat16": 2500.0, "float16": 2500.0, "float8_e4m3fn": 5000.0}
+TRIAD_ELEMENTS = 1 << 28
+TRAFFIC_SUMMARY = ROOT / "profiles" / "stream_triad_f32_2p28_traffic.txt"
+
+
+def _log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def read_traffic() -> dict | None:
+    """HBM bytes per triad launch from the committed rocprofv3 counter summary.
+
+    The summary holds a line `traffic_bytes_per_launch: <int>` derived from
+    FETCH_SIZE + WRITE_SIZE scaled by the copy-kernel calibration factor.
+    """
+    if not TRAFFIC_SUMMARY.exists():
+        return None
+    for line in TRAFFIC_SUMMARY.read_text(encoding="utf-8").splitlines():
+        if line.startswith("traffic_bytes_per_launch:"):
+            return {"bytes": int(float(line.split(":", 1)[1])), "source": str(TRAFFIC_SUMMARY.relative_to(ROOT))}
+    return None
+
+
+def bench_triad(torch, lib, capi, steps: int, warmup: int) -> dict:
+    n = TRIAD_ELEMENTS
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(0)
+    b = torch.empty(n, device=dev, dtype=torch.float32).uniform_(-1.0, 1.0, generator=gen)
+    c = torch.empty(n, device=dev, dtype=torch.float32).uniform_(-1.0, 1.0, generator=gen)
+    a = torch.empty_like(b)
+    stream = torch.cuda.current_stream(dev)
+    handle = stream.cuda_stream
+
+    def step() -> None:
+        lib.stream(capi.OP_TRIAD, capi.DT_FLOAT32, a.data_ptr(), b.data_ptr(), c.data_ptr(), n, 3.0, 0, handle)
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    start_ev = torch.cuda.Event(enable_timing=True)
+    stop_ev = torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    start_ev.record(stream)
+    for _ in range(steps):
+        step()
+    stop_ev.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    event_s = start_ev.elapsed_time(stop_ev) / 1000.0 / steps
+
+    # in-run parity against the torch GPU op (1 ulp bound of the stream configuration)
+    from teamredbench_amd.parity import stream_parity
+
+    ref = torch.add(b, c, alpha=3.0)
+    parity = stream_parity(torch, "triad", a, ref)
+    del ref
+    moved = 3 * 4 * n
+    return {
+        "wall_s_per_step": wall / steps,
+        "event_s_per_launch": event_s,
+        "moved_bytes": moved,
+        "parity": parity,
+        "info": lib.stream_info(capi.OP_TRIAD, capi.DT_FLOAT32, n),
+    }
+
+
+def bench_gemm(torch, lib, capi, dtype: str, size: int, warmup: int, iterations: int) -> dict:
+    from teamredbench_amd.parity import gemm_parity
+    from teamredbench_amd.utils import seeded_gemm_operands
+
+    dev = torch.device("cuda:0")
+    m = n = k = size
+    a, b, sa, sb = seeded_gemm_operands(torch, m, n, k, dtype, dev, seed=0)
+    out_dtype = torch.float16 if dtype == "float16" else torch.bfloat16
+    c = torch.empty((m, n), device=dev, dtype=out_dtype)
+    dt = capi.DTYPES[dtype]
+    ws_bytes = lib.gemm_workspace_size(dt, m, n, k)
+    ws = torch.empty(max(ws_bytes, 1), device=dev, dtype=torch.uint8)
+    handle = torch.cuda.current_stream(dev).cuda_stream
+    secs = lib.time_gemm(dt, a.data_ptr(), b.data_ptr(), c.data_ptr(), m, n, k, sa, sb, ws.data_ptr(), ws_bytes,
+                         warmup, iterations, handle)
+    rows = torch.randperm(m, generator=torch.Generator().manual_seed(0))[:256].to(dev)
+    ref = (a[rows].float() * sa) @ (b.float() * sb)
+    parity = gemm_parity(torch, dtype, c[rows].float(), ref)
+    flops = 2.0 * m * n * k
+    tflops = flops / secs / 1e12
+    info = lib.gemm_info(dt, m, n, k)
+    del a, b, c, ws, ref
+    torch.cuda.empty_cache()
+    return {
+        "shape": [m, n, k],
+        "latency_us": secs * 1e6,
+        "achieved_tflops": tflops,
+        "mfu_pct": 100.0 * tflops / MFMA_PEAK_TFLOPS[dtype],
+        "parity": {**parity, "rows_checked": 256},
+        "implementation": info.get("implementation"),
+    }
+
+
+def cpu_baseline(seconds: float) -> dict:
+    """The reference torch op on CPU tensors (oracle restatement of hbm.py:29-39)."""
+    import torch
+
+    from oracle import reference_path as rp
+
+    cores = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    cores = max(1, min(cores, 16))
+    torch.set_num_threads(cores)
+    n = TRIAD_ELEMENTS
+    b, c = rp.stream_inputs(n, "float32", seed=0)
+    a = torch.empty_like(b)
+    for _ in range(2):
+        rp.run_mode("triad", b, a, c, 3.0)
+    iters = 0
+    t0 = time.perf_counter()
+    while True:
+        rp.run_mode("triad", b, a, c, 3.0)
+        iters += 1
+        elapsed = time.perf_counter() - t0
+        if elapsed >= seconds:
+            break
+    per = elapsed / iters
+    return {
+        "value": 3 * 4 * n / per / 1e9,
+        "unit": "GB/s",
+        "cores": cores,
+        "kind": "port",
+        "sample": (f"fp32 triad over 2^28 elements per array, torch.add(b, c, alpha=3.0, out=a) on CPU tensors, "
+                   f"{iters} iterations in {elapsed:.1f} s after 2 warmup"),
+    }
+
+
+def main() -> int:
+    parser = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    parser.add_argument("--gpus", type=int, default=1)
+    parser.add_argument("--steps", type=int, default=50)
+    parser.add_argument("--warmup", type=int, default=10)
+    parser.add_argument("--no-gemm", action="store_true", help="skip the 8192^3 GEMM measurements")
+    parser.add_argument("--gemm-iterations", type=int, default=20)
+    parser.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline sample length (0 = skip)")
+    args = parser.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); the stream and GEMM paths shard "
+              "with no exchange, so N GPUs = N independent single-GPU runs.", file=sys.stderr)
+        return 2
+    if args.steps < 1 or args.warmup < 0:
+        parser.error("--steps must be >= 1 and --warmup >= 0")
+
+    import torch
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a visible MI355X (torch.cuda.is_available() is False)", file=sys.stderr)
+        return 1
+    torch.cuda.set_device(0)
+    from teamredbench_amd.native import capi
+
+    lib = capi.load_library()  # raises if the HIP library is missing or stale: no fallback
+
+    _log(f"triad fp32 2^28: warmup {args.warmup}, steps {args.steps}")
+    triad = bench_triad(torch, lib, capi, args.steps, args.warmup)
+    value = triad["moved_bytes"] / triad["wall_s_per_step"] / 1e9
+    achieved = triad["moved_bytes"] / triad["event_s_per_launch"] / 1e9
+    _log(f"triad: {value:.1f} GB/s wall, {achieved:.1f} GB/s events, parity {triad['parity']}")
+    torch.cuda.empty_cache()
+
+    gemm = {}
+    if not args.no_gemm:
+        for dtype in ("bfloat16", "float8_e4m3fn"):
+            _log(f"gemm {dtype} 8192^3")
+            gemm[dtype] = bench_gemm(torch, lib, capi, dtype, 8192, warmup=3, iterations=args.gemm_iterations)
+            _log(f"gemm {dtype}: {gemm[dtype]['achieved_tflops']:.1f} TFLOPS ({gemm[dtype]['mfu_pct']:.1f}% MFU)")
+
+    baseline = None
+    if args.cpu_seconds > 0:
+        _log(f"cpu baseline: {args.cpu_seconds:.0f} s sample")
+        baseline = cpu_baseline(args.cpu_seconds)
+
+    traffic = read_traffic()
+    line = {
+        "metric": "triad HBM GB/s & % peak; bf16/fp8 GEMM TFLOPS & MFU% at 8192^3",
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": triad["wall_s_per_step"] * 1e3,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic: b, c ~ uniform[-1, 1] fp32 from seed 0, resident in HBM",
+        "config": {
+            "workload": "stream triad a = b + 3*c, fp32, 2^28 elements per array (3 GiB moved per step)",
+            "elements": TRIAD_ELEMENTS,
+            "element_dtype": "float32",
+            "scale": 3.0,
+        },
+        "hbm_efficiency_pct": round(100.0 * value / HBM_PEAK_GBPS, 2),
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(achieved, 2),
+            "peak": HBM_PEAK_GBPS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBPS, 4),
+            "traffic": traffic["bytes"] if traffic else None,
+            "algorithmic_bytes": triad["moved_bytes"],
+            "kernel": triad["info"].get("implementation"),
+        },
+        "parity": triad["parity"],
+        "kernel_info": triad["info"],
+        "gemm": gemm or None,
+        "cpu_baseline": baseline,
+    }
+    if traffic:
+        line["roofline"]["traffic_source"] = traffic["source"]
+    print(json.dumps(line), flush=True)
+    ok = triad["parity"]["passed"] and all(g["parity"]["passed"] for g in gemm.values())
+    return 0 if ok else 3
+
+
+if __name__ == "__main__":
+    sys.exit(main())

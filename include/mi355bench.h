@@ -1,0 +1,153 @@
+/*
+ * mi355bench.h -- C ABI of libmi355bench.so, the gfx950 (MI355X) stream and
+ * GEMM kernels behind TeamRedBench's `backend: native` path.
+ *
+ * The reference crosses into native code through a subprocess: Python builds
+ * argv, runs a hipcc-built executable per case and parses one JSON line from
+ * its stdout (src/teamredbench/native/runtime.py:276-291,
+ * src/teamredbench/benchmarks/hbm.py:95-116, src/teamredbench/benchmarks/mfu.py:106-125).
+ * This library replaces that process boundary with in-process calls. Every
+ * entry point below names the reference code it replaces.
+ *
+ * Conventions (all entry points):
+ *   - Plain pointers and sizes only. Device buffers are owned by the caller;
+ *     the library never allocates or frees device memory except the hipEvents
+ *     used by the mb_time_* entry points.
+ *   - `stream` is a hipStream_t passed as void* (NULL = the null stream).
+ *     Work is enqueued asynchronously; nothing synchronises except mb_time_*.
+ *   - Return 0 on success, a negative MB_ERR_* for a rejected argument, or a
+ *     positive hipError_t from the HIP runtime. On any non-zero return,
+ *     mb_last_error() describes the failure (thread-local string).
+ *   - Thread-safe and reentrant; per-device properties are cached once.
+ */
+#ifndef MI355BENCH_H
+#define MI355BENCH_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MB_ABI_VERSION 1
+
+/* Status codes (negative = rejected by the library before any launch). */
+#define MB_OK 0
+#define MB_ERR_INVALID_ARG -1  /* null pointer, negative size, bad enum */
+#define MB_ERR_UNSUPPORTED -2  /* dtype/op combination not implemented */
+#define MB_ERR_SHAPE -3        /* shape the kernel family cannot take */
+#define MB_ERR_WORKSPACE -4    /* workspace missing or too small */
+#define MB_ERR_DEVICE -5       /* current device is not gfx950 */
+
+/* Stream operations; semantics of src/teamredbench/benchmarks/hbm.py:29-39. */
+#define MB_OP_COPY 0  /* dst = b                 (torch: dst.copy_(src))          */
+#define MB_OP_SCALE 1 /* dst = s * b             (torch: torch.mul(src, s, out=dst)) */
+#define MB_OP_TRIAD 2 /* dst = b + s * c         (torch: torch.add(src, aux, alpha=s, out=dst)) */
+
+/* Element types (names follow src/teamredbench/dtypes.py:16-31). */
+#define MB_DT_FLOAT32 0
+#define MB_DT_BFLOAT16 1
+#define MB_DT_FLOAT16 2
+#define MB_DT_FLOAT64 3
+#define MB_DT_INT8 4           /* copy only */
+#define MB_DT_FLOAT8_E4M3FN 5  /* GEMM inputs only; output is bfloat16 */
+
+/* Kinds for mb_kernel_info. */
+#define MB_KIND_STREAM 0
+#define MB_KIND_GEMM 1
+
+/*
+ * mb_stream -- one launch of a stream kernel over n elements.
+ *
+ * Replaces the per-iteration launch in the reference executable's
+ * run_kernel<T>::launch_once (native/kernels/hbm_bandwidth.hip.cpp:371-388):
+ * hipMemcpyAsync for copy, scale_kernel<T> / triad_kernel<T> otherwise.
+ *
+ * dst, b: n elements of `dtype`; c: n elements for TRIAD, ignored (may be NULL)
+ * otherwise. Any n (0 is a no-op) and any element alignment: 16-byte aligned
+ * buffers take the vector kernel plus a scalar tail, others a scalar kernel.
+ * Arithmetic: fp32 math with one round-to-nearest-even to the element type
+ * (fp64 math for float64); TRIAD is one fused multiply-add, fma(s, c, b).
+ * blocks_per_cu: grid = min(CUs * blocks_per_cu, work); <= 0 selects the
+ * tuned default (the reference's --blocks-per-cu override, hbm.py:111-114).
+ */
+int mb_stream(int op, int dtype, void* dst, const void* b, const void* c,
+              uint64_t n, double s, int blocks_per_cu, void* stream);
+
+/*
+ * mb_time_stream -- warmup + event-timed loop of mb_stream launches.
+ *
+ * Replaces the timing body of run_kernel<T> (hbm_bandwidth.hip.cpp:390-425):
+ * `warmup` launches, a stream synchronise, then `iterations` launches between
+ * two hipEvents recorded on `stream`; *elapsed_s = event time / iterations.
+ * Synchronises `stream` before returning.
+ */
+int mb_time_stream(int op, int dtype, void* dst, const void* b, const void* c,
+                   uint64_t n, double s, int blocks_per_cu, int warmup,
+                   int iterations, void* stream, double* elapsed_s);
+
+/*
+ * mb_gemm -- C = A * B, row-major, fp32 accumulation.
+ *
+ * Replaces the launch of mfma_gemm_lowp_kernel<T>
+ * (native/kernels/mfu_gemm_lowp.hip.hpp:423-445) and its untimed
+ * pack_b_tiles_kernel<T> pre-pass (:396-409): B is consumed as given,
+ * row-major K x N, with no re-layout outside the timed kernel.
+ *
+ * dtype  A (M x K)   B (K x N)   C (M x N)   epilogue
+ * BF16   bf16        bf16        bf16        RNE(acc)
+ * F16    fp16        fp16        fp16        RNE(acc)
+ * FP8    e4m3fn      e4m3fn      bf16        RNE(scale_a * scale_b * acc)
+ * scale_a/scale_b are the fp8 per-tensor dequantisation scales (ignored for
+ * bf16/f16). Leading dimensions are K, N and N. Any M, N, K >= 1 whose rows
+ * keep 16-byte alignment (K*elem and N*elem multiples of 16) with 16-byte
+ * aligned base pointers; other shapes return MB_ERR_SHAPE.
+ * workspace: device scratch of at least mb_gemm_workspace_size() bytes (may
+ * be NULL when that size is 0). The kernels leave it in a state the next
+ * call can use without clearing.
+ */
+int mb_gemm(int dtype, const void* A, const void* B, void* C, int64_t M,
+            int64_t N, int64_t K, float scale_a, float scale_b, void* workspace,
+            size_t workspace_bytes, void* stream);
+
+/* Workspace bytes mb_gemm needs for this dtype and shape (0 if none). */
+size_t mb_gemm_workspace_size(int dtype, int64_t M, int64_t N, int64_t K);
+
+/*
+ * mb_time_gemm -- warmup + event-timed loop of mb_gemm launches.
+ *
+ * Replaces the timing body of run_low_precision_kernel<T>
+ * (mfu_gemm_lowp.hip.hpp:447-485); same contract as mb_time_stream.
+ */
+int mb_time_gemm(int dtype, const void* A, const void* B, void* C, int64_t M,
+                 int64_t N, int64_t K, float scale_a, float scale_b,
+                 void* workspace, size_t workspace_bytes, int warmup,
+                 int iterations, void* stream, double* elapsed_s);
+
+/*
+ * mb_kernel_info -- JSON object describing the kernel configuration the
+ * library picks for a case, written NUL-terminated into json[0..cap).
+ *
+ * Replaces the "metadata" object the reference executables print
+ * (hbm_bandwidth.hip.cpp:431-436; mfu_gemm_lowp.hip.hpp:492-509), keeping
+ * its keys (implementation, threads_per_block, blocks_per_cu, tile_m/n/k,
+ * wave_grid_*, wave_tile_*, frag_*, k_stages ...).
+ * kind = MB_KIND_STREAM: a = op, b = dtype, m = n elements, n = blocks_per_cu.
+ * kind = MB_KIND_GEMM:   a = dtype, m, n, k = shape (b ignored).
+ * Returns MB_ERR_INVALID_ARG if json is NULL or cap is too small.
+ */
+int mb_kernel_info(int kind, int a, int b, int64_t m, int64_t n, int64_t k,
+                   char* json, size_t cap);
+
+/* Description of the last failure on the calling thread ("" if none). */
+const char* mb_last_error(void);
+
+/* MB_ABI_VERSION of the loaded library. */
+int mb_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MI355BENCH_H */

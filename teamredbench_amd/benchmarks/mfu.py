@@ -1,0 +1,228 @@
+"""``mfu`` benchmark: dense GEMM C = A * B and its model-FLOPs utilisation.
+
+API and record shape follow src/teamredbench/benchmarks/mfu.py:
+  params: backend (torch|native), dtypes, shapes [[m, n, k], ...] (default
+          4096^3 and 8192^3), warmup (10), iterations (50), native.{...}
+  extension params: seed (default 0), verify (compare against torch,
+          default true; at most `verify_max_rows` rows of C, default 4096)
+  record: case "gemm_<m>x<n>x<k>"; raw_metrics elapsed_s / achieved_ops
+          (= matmul_ops_factor * m * n * k) / peak_tops, plus gemm_bytes
+          ((mk + kn) * in_bytes + mn * out_bytes) for the effective-GB/s metric.
+A dtype with matmul_ops_factor 0, or without a peak in the hardware profile,
+yields a skipped record (mfu.py:81-104).
+
+backend "native" with a built-in kernel calls libmi355bench.so (mb_time_gemm,
+event-timed on torch's current stream). B is consumed row-major as given:
+unlike the reference executable there is no untimed re-layout of B
+(native/kernels/mfu_gemm_lowp.hip.hpp:396-409). Inputs are seeded:
+bf16/fp16 ~ normal(0, 1/sqrt(k)); fp8 e4m3fn ~ normal(0, 1) quantised per
+tensor with amax -> 448, bf16 output with the dequantisation scales applied
+in the fp32 epilogue.
+"""
+from __future__ import annotations
+
+from typing import Any
+
+from teamredbench_amd.benchmarks.base import Benchmark, BenchmarkRecord
+from teamredbench_amd.benchmarks.native_exec import ExecutableCase, run_executable_cases
+from teamredbench_amd.device import rocm_device_available
+from teamredbench_amd.native import capi
+from teamredbench_amd.native.runtime import resolve_native_kernel
+from teamredbench_amd.parity import gemm_parity
+from teamredbench_amd.registry import register_benchmark
+from teamredbench_amd.utils import make_tensor, seeded_gemm_operands, timed_iterations
+
+DEFAULT_SHAPES = [
+    [4096, 4096, 4096],
+    [8192, 8192, 8192],
+]
+
+INFINITY_CACHE_BYTES = 256 * 1024 * 1024
+
+
+def gemm_bytes(m: int, n: int, k: int, in_bytes: int, out_bytes: int) -> int:
+    """Algorithmic bytes of one GEMM: read A and B once, write C once."""
+    return (m * k + k * n) * in_bytes + m * n * out_bytes
+
+
+@register_benchmark("mfu")
+class MfuBenchmark(Benchmark):
+    default_metrics = ["achieved_tops", "mfu_pct", "latency_us"]
+
+    def _common_params(self) -> tuple[int, int, list[list[int]]]:
+        warmup = int(self.params.get("warmup", 10))
+        iterations = int(self.params.get("iterations", 50))
+        shapes = list(self.params.get("shapes", DEFAULT_SHAPES))
+        return warmup, iterations, shapes
+
+    def _gate(self, spec, peak_tops) -> str | None:
+        if spec.matmul_ops_factor == 0:
+            return "MFU is not defined for this dtype."
+        if peak_tops is None:
+            return "Missing peak_compute_tops entry for dtype in hardware profile."
+        return None
+
+    # ------------------------------------------------------------ native
+    def _run_native(self) -> list[BenchmarkRecord]:
+        kernel = resolve_native_kernel(
+            benchmark=self.name,
+            params=self.params,
+            suite_path=self.context.suite_path,
+            repo_root=self.context.repo_root,
+            default_kernel="mfu_hipblas",
+        )
+        if kernel.in_process:
+            return self._run_capi(kernel.name)
+        return self._run_executable(kernel)
+
+    def _run_executable(self, kernel) -> list[BenchmarkRecord]:
+        warmup, iterations, shapes = self._common_params()
+        cases: list[ExecutableCase] = []
+        for spec in self.selected_dtype_specs():
+            peak_tops = self.context.hardware_profile.peak_compute_tops.get(spec.name)
+            for shape in shapes:
+                m, n, k = (int(d) for d in shape)
+                metadata = {"backend": "native", "kernel": kernel.name, "m": m, "n": n, "k": k}
+                gate = self._gate(spec, peak_tops)
+                argv = None if gate else [
+                    "--dtype", spec.name, "--m", str(m), "--n", str(n), "--k", str(k), "--warmup", str(warmup),
+                    "--iterations", str(iterations), "--device-id", str(self.context.device_id),
+                ]
+                ops = spec.matmul_ops_factor * m * n * k
+
+                def defaults(raw: dict[str, Any], ops: int = ops, peak=peak_tops) -> None:
+                    raw.setdefault("achieved_ops", ops)
+                    raw.setdefault("peak_tops", peak)
+
+                cases.append(ExecutableCase(f"gemm_{m}x{n}x{k}", spec.name, metadata, argv, defaults, gate))
+        return run_executable_cases(self, kernel, cases)
+
+    def _run_capi(self, kernel_name: str) -> list[BenchmarkRecord]:
+        warmup, iterations, shapes = self._common_params()
+        seed = int(self.params.get("seed", 0))
+        verify = bool(self.params.get("verify", True))
+        verify_rows = int(self.params.get("verify_max_rows", 4096))
+        plan = []
+        for spec in self.selected_dtype_specs():
+            peak_tops = self.context.hardware_profile.peak_compute_tops.get(spec.name)
+            for shape in shapes:
+                m, n, k = (int(d) for d in shape)
+                meta = {"backend": "native", "kernel": kernel_name, "m": m, "n": n, "k": k}
+                plan.append((spec, peak_tops, m, n, k, f"gemm_{m}x{n}x{k}", meta))
+
+        try:
+            lib = capi.load_library()
+        except capi.NativeLibraryError as exc:
+            return [self.skip(case=c, dtype=s.name, error=str(exc), metadata=md) for s, _, _, _, _, c, md in plan]
+        torch = self.context.torch_module
+        if not rocm_device_available(torch):
+            return [self.skip(case=c, dtype=s.name, error="No ROCm device visible to PyTorch.", metadata=md)
+                    for s, _, _, _, _, c, md in plan]
+        self.set_device()
+
+        records: list[BenchmarkRecord] = []
+        for spec, peak_tops, m, n, k, case, meta in plan:
+            gate = self._gate(spec, peak_tops)
+            if gate is None and spec.name not in capi.GEMM_DTYPES:
+                gate = f"unsupported dtype for native GEMM kernel: {spec.name}"
+            if gate:
+                records.append(self.skip(case=case, dtype=spec.name, error=gate, metadata=meta))
+                continue
+            try:
+                records.append(self._capi_case(lib, torch, spec, peak_tops, m, n, k, case, meta, warmup, iterations,
+                                               seed, verify, verify_rows))
+            except (capi.NativeLibraryError, RuntimeError) as exc:
+                records.append(self.skip(case=case, dtype=spec.name, error=str(exc), metadata=meta))
+            finally:
+                torch.cuda.empty_cache()
+        return records
+
+    def _capi_case(self, lib, torch, spec, peak_tops, m, n, k, case, meta, warmup, iterations, seed, verify,
+                   verify_rows) -> BenchmarkRecord:
+        device = self.device
+        a, b, sa, sb = seeded_gemm_operands(torch, m, n, k, spec.name, device, seed)
+        out_dtype = torch.float16 if spec.name == "float16" else torch.bfloat16
+        c = torch.empty((m, n), device=device, dtype=out_dtype)
+        dt = capi.DTYPES[spec.name]
+        ws_bytes = lib.gemm_workspace_size(dt, m, n, k)
+        ws = torch.empty(ws_bytes, device=device, dtype=torch.uint8) if ws_bytes else None
+        stream = torch.cuda.current_stream(device).cuda_stream
+        elapsed = lib.time_gemm(dt, a.data_ptr(), b.data_ptr(), c.data_ptr(), m, n, k, sa, sb,
+                                ws.data_ptr() if ws is not None else None, ws_bytes, warmup, iterations, stream)
+        meta = {**meta, **lib.gemm_info(dt, m, n, k)}
+        if spec.name == "float8_e4m3fn":
+            meta["scale_a"], meta["scale_b"] = sa, sb
+        in_bytes = spec.bytes_per_element
+        moved = gemm_bytes(m, n, k, in_bytes, c.element_size())
+        meta["cache_resident_b"] = k * n * in_bytes <= INFINITY_CACHE_BYTES
+        if verify:
+            rows = min(m, verify_rows)
+            ref = (a[:rows].float() * sa) @ (b.float() * sb)
+            meta["parity"] = gemm_parity(torch, spec.name, c[:rows].float(), ref)
+            meta["parity"]["rows_checked"] = rows
+            del ref
+        return self.emit_record(
+            BenchmarkRecord(
+                benchmark=self.name,
+                case=case,
+                dtype=spec.name,
+                raw_metrics={
+                    "elapsed_s": elapsed,
+                    "achieved_ops": spec.matmul_ops_factor * m * n * k,
+                    "peak_tops": peak_tops,
+                    "gemm_bytes": moved,
+                },
+                metadata=meta,
+            )
+        )
+
+    # ------------------------------------------------------------- torch
+    def _run_torch(self) -> list[BenchmarkRecord]:
+        if self.context.torch_module is None:
+            return [self.skip(case="global", dtype="n/a", error="PyTorch is not installed.")]
+        torch = self.torch
+        if not rocm_device_available(torch):
+            return [self.skip(case="global", dtype="n/a", error="No ROCm device visible to PyTorch.")]
+        self.set_device()
+        warmup, iterations, shapes = self._common_params()
+        records: list[BenchmarkRecord] = []
+        for spec in self.selected_dtype_specs():
+            peak_tops = self.context.hardware_profile.peak_compute_tops.get(spec.name)
+            for shape in shapes:
+                m, n, k = (int(d) for d in shape)
+                case = f"gemm_{m}x{n}x{k}"
+                meta = {"backend": "torch", "m": m, "n": n, "k": k}
+                gate = self._gate(spec, peak_tops)
+                if gate:
+                    records.append(self.skip(case=case, dtype=spec.name, error=gate, metadata=meta))
+                    continue
+                try:
+                    a = make_tensor(torch, spec, (m, k), self.device)
+                    b = make_tensor(torch, spec, (k, n), self.device)
+                    out = torch.empty((m, n), device=self.device, dtype=getattr(torch, spec.torch_attr))
+                    elapsed = timed_iterations(lambda: torch.mm(a, b, out=out), torch_module=torch, warmup=warmup,
+                                               iterations=iterations)
+                except Exception as exc:  # noqa: BLE001 -- any failure skips this case only
+                    records.append(self.skip(case=case, dtype=spec.name, error=str(exc), metadata=meta))
+                    continue
+                records.append(
+                    self.emit_record(
+                        BenchmarkRecord(
+                            benchmark=self.name,
+                            case=case,
+                            dtype=spec.name,
+                            raw_metrics={"elapsed_s": elapsed, "achieved_ops": spec.matmul_ops_factor * m * n * k,
+                                         "peak_tops": peak_tops},
+                            metadata=meta,
+                        )
+                    )
+                )
+        return records
+
+    def run(self) -> list[BenchmarkRecord]:
+        backend = str(self.params.get("backend", "torch")).lower()
+        if backend == "torch":
+            return self._run_torch()
+        if backend == "native":
+            return self._run_native()
+        raise KeyError(f"Unknown MFU backend: {backend}")

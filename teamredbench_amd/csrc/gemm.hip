@@ -1,0 +1,36 @@
+// GEMM dispatch: picks the kernel family for a (dtype, M, N, K) case and
+// forwards the launch. Validation of dtype and sizes lives here.
+#include "gemm_common.hpp"
+
+namespace mb {
+
+int gemm_plan(int dtype, int64_t M, int64_t N, int64_t K, const DeviceProps& props,
+              GemmPlan* plan) {
+    (void)props;
+    if (dtype != MB_DT_BFLOAT16 && dtype != MB_DT_FLOAT16 && dtype != MB_DT_FLOAT8_E4M3FN) {
+        set_error("GEMM supports bfloat16, float16 and float8_e4m3fn (got %s)", dtype_name(dtype));
+        return MB_ERR_UNSUPPORTED;
+    }
+    if (M < 1 || N < 1 || K < 1) {
+        set_error("GEMM sizes must be >= 1 (M=%lld N=%lld K=%lld)", (long long)M, (long long)N,
+                  (long long)K);
+        return MB_ERR_INVALID_ARG;
+    }
+    return gemm_generic_plan(dtype, M, N, K, plan);
+}
+
+int gemm_launch(int dtype, const void* A, const void* B, void* C, int64_t M, int64_t N, int64_t K,
+                float scale_a, float scale_b, void* workspace, const GemmPlan& plan,
+                hipStream_t stream) {
+    (void)workspace;
+    const float alpha = dtype == MB_DT_FLOAT8_E4M3FN ? scale_a * scale_b : 1.0f;
+    switch (plan.variant) {
+        case kVariantGeneric:
+            return gemm_generic_launch(dtype, A, B, C, M, N, K, alpha, stream);
+        default:
+            set_error("GEMM plan variant %d not available", plan.variant);
+            return MB_ERR_UNSUPPORTED;
+    }
+}
+
+}  // namespace mb

@@ -1,0 +1,213 @@
+"""ctypes binding of libmi355bench.so (C ABI in include/mi355bench.h).
+
+This is the in-process replacement of the reference's executable contract
+(argv in, one JSON line out; src/teamredbench/native/runtime.py:249-291).
+Tensors are passed as raw device pointers (``tensor.data_ptr()``) together
+with the HIP stream torch is using, so torch owns every allocation and the
+library only enqueues kernels.
+
+Loading never falls back to anything else: if the shared library is missing
+or was built from other sources, :func:`load_library` raises
+:class:`NativeLibraryError`, and callers surface that as the error of a
+skipped record, the way the reference surfaces a failed hipcc build
+(src/teamredbench/benchmarks/hbm.py:59-81).
+"""
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+import json
+import os
+from pathlib import Path
+import threading
+from typing import Any
+
+from teamredbench_amd.native import build as _build
+
+MB_OK = 0
+MB_ERR_INVALID_ARG = -1
+MB_ERR_UNSUPPORTED = -2
+MB_ERR_SHAPE = -3
+MB_ERR_WORKSPACE = -4
+MB_ERR_DEVICE = -5
+
+OP_COPY, OP_SCALE, OP_TRIAD = 0, 1, 2
+OPS = {"copy": OP_COPY, "scale": OP_SCALE, "triad": OP_TRIAD}
+
+DT_FLOAT32, DT_BFLOAT16, DT_FLOAT16, DT_FLOAT64, DT_INT8, DT_FLOAT8_E4M3FN = 0, 1, 2, 3, 4, 5
+DTYPES = {
+    "float32": DT_FLOAT32,
+    "bfloat16": DT_BFLOAT16,
+    "float16": DT_FLOAT16,
+    "float64": DT_FLOAT64,
+    "int8": DT_INT8,
+    "float8_e4m3fn": DT_FLOAT8_E4M3FN,
+}
+STREAM_DTYPES = ("float32", "bfloat16", "float16", "float64", "int8")
+GEMM_DTYPES = ("bfloat16", "float16", "float8_e4m3fn")
+
+KIND_STREAM, KIND_GEMM = 0, 1
+
+# Every symbol include/mi355bench.h declares, with (restype, argtypes).
+_u64, _i64, _vp, _cvp = ctypes.c_uint64, ctypes.c_int64, ctypes.c_void_p, ctypes.c_void_p
+SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
+    "mb_abi_version": (ctypes.c_int, []),
+    "mb_last_error": (ctypes.c_char_p, []),
+    "mb_stream": (
+        ctypes.c_int,
+        [ctypes.c_int, ctypes.c_int, _vp, _cvp, _cvp, _u64, ctypes.c_double, ctypes.c_int, _vp],
+    ),
+    "mb_time_stream": (
+        ctypes.c_int,
+        [
+            ctypes.c_int, ctypes.c_int, _vp, _cvp, _cvp, _u64, ctypes.c_double, ctypes.c_int,
+            ctypes.c_int, ctypes.c_int, _vp, ctypes.POINTER(ctypes.c_double),
+        ],
+    ),
+    "mb_gemm": (
+        ctypes.c_int,
+        [
+            ctypes.c_int, _cvp, _cvp, _vp, _i64, _i64, _i64, ctypes.c_float, ctypes.c_float, _vp,
+            ctypes.c_size_t, _vp,
+        ],
+    ),
+    "mb_gemm_workspace_size": (ctypes.c_size_t, [ctypes.c_int, _i64, _i64, _i64]),
+    "mb_time_gemm": (
+        ctypes.c_int,
+        [
+            ctypes.c_int, _cvp, _cvp, _vp, _i64, _i64, _i64, ctypes.c_float, ctypes.c_float, _vp,
+            ctypes.c_size_t, ctypes.c_int, ctypes.c_int, _vp, ctypes.POINTER(ctypes.c_double),
+        ],
+    ),
+    "mb_kernel_info": (
+        ctypes.c_int,
+        [ctypes.c_int, ctypes.c_int, ctypes.c_int, _i64, _i64, _i64, ctypes.c_char_p, ctypes.c_size_t],
+    ),
+}
+
+ABI_VERSION = 1
+
+
+class NativeLibraryError(RuntimeError):
+    """The shared library is missing, stale, or a call into it failed."""
+
+    def __init__(self, message: str, status: int | None = None):
+        super().__init__(message)
+        self.status = status
+
+
+@dataclass
+class NativeLibrary:
+    path: Path
+    handle: ctypes.CDLL
+
+    # ---- helpers -----------------------------------------------------------
+    def _check(self, status: int, what: str) -> None:
+        if status != MB_OK:
+            detail = (self.handle.mb_last_error() or b"").decode("utf-8", "replace")
+            raise NativeLibraryError(f"{what} failed with status {status}: {detail}", status)
+
+    # ---- stream ------------------------------------------------------------
+    def stream(self, op: int, dtype: int, dst: int, b: int, c: int | None, n: int, s: float,
+               blocks_per_cu: int = 0, stream: int | None = None) -> None:
+        status = self.handle.mb_stream(op, dtype, dst, b, c or None, n, float(s), int(blocks_per_cu), stream or None)
+        self._check(status, "mb_stream")
+
+    def time_stream(self, op: int, dtype: int, dst: int, b: int, c: int | None, n: int, s: float,
+                    blocks_per_cu: int, warmup: int, iterations: int, stream: int | None = None) -> float:
+        out = ctypes.c_double(0.0)
+        status = self.handle.mb_time_stream(
+            op, dtype, dst, b, c or None, n, float(s), int(blocks_per_cu), int(warmup), int(iterations),
+            stream or None, ctypes.byref(out),
+        )
+        self._check(status, "mb_time_stream")
+        return out.value
+
+    # ---- gemm --------------------------------------------------------------
+    def gemm_workspace_size(self, dtype: int, m: int, n: int, k: int) -> int:
+        return int(self.handle.mb_gemm_workspace_size(dtype, m, n, k))
+
+    def gemm(self, dtype: int, a: int, b: int, c: int, m: int, n: int, k: int, scale_a: float = 1.0,
+             scale_b: float = 1.0, workspace: int | None = None, workspace_bytes: int = 0,
+             stream: int | None = None) -> None:
+        status = self.handle.mb_gemm(
+            dtype, a, b, c, m, n, k, float(scale_a), float(scale_b), workspace or None, int(workspace_bytes),
+            stream or None,
+        )
+        self._check(status, "mb_gemm")
+
+    def time_gemm(self, dtype: int, a: int, b: int, c: int, m: int, n: int, k: int, scale_a: float,
+                  scale_b: float, workspace: int | None, workspace_bytes: int, warmup: int, iterations: int,
+                  stream: int | None = None) -> float:
+        out = ctypes.c_double(0.0)
+        status = self.handle.mb_time_gemm(
+            dtype, a, b, c, m, n, k, float(scale_a), float(scale_b), workspace or None, int(workspace_bytes),
+            int(warmup), int(iterations), stream or None, ctypes.byref(out),
+        )
+        self._check(status, "mb_time_gemm")
+        return out.value
+
+    # ---- metadata ----------------------------------------------------------
+    def kernel_info(self, kind: int, a: int, b: int, m: int, n: int, k: int) -> dict[str, Any]:
+        buf = ctypes.create_string_buffer(4096)
+        status = self.handle.mb_kernel_info(kind, a, b, m, n, k, buf, len(buf))
+        self._check(status, "mb_kernel_info")
+        return json.loads(buf.value.decode("utf-8"))
+
+    def stream_info(self, op: int, dtype: int, n: int, blocks_per_cu: int = 0) -> dict[str, Any]:
+        return self.kernel_info(KIND_STREAM, op, dtype, n, blocks_per_cu, 0)
+
+    def gemm_info(self, dtype: int, m: int, n: int, k: int) -> dict[str, Any]:
+        return self.kernel_info(KIND_GEMM, dtype, 0, m, n, k)
+
+
+_lock = threading.Lock()
+_cache: dict[Path, NativeLibrary] = {}
+
+
+def library_path() -> Path:
+    override = os.environ.get("MI355BENCH_LIBRARY")
+    return Path(override).resolve() if override else _build.library_path()
+
+
+def bind(handle: ctypes.CDLL) -> None:
+    for name, (restype, argtypes) in SIGNATURES.items():
+        fn = getattr(handle, name)
+        fn.restype = restype
+        fn.argtypes = argtypes
+
+
+def load_library(path: str | Path | None = None, *, check_digest: bool = True) -> NativeLibrary:
+    """Load (once per path) and bind libmi355bench.so.
+
+    Raises NativeLibraryError when the file is absent, was built from sources
+    other than the ones in this tree (BUILD_DIGEST mismatch), or exports a
+    different ABI version.
+    """
+    lib_path = Path(path).resolve() if path else library_path()
+    with _lock:
+        if lib_path in _cache:
+            return _cache[lib_path]
+        if not lib_path.exists():
+            raise NativeLibraryError(
+                f"{lib_path} is not built; run `python -m teamredbench_amd.native.build` "
+                "(or __graft_entry__.build())"
+            )
+        if check_digest and path is None and os.environ.get("MI355BENCH_LIBRARY") is None:
+            stamp = lib_path.parent / "BUILD_DIGEST"
+            recorded = stamp.read_text(encoding="utf-8").strip() if stamp.exists() else ""
+            if recorded != _build.source_digest():
+                raise NativeLibraryError(
+                    f"{lib_path} was built from different sources than teamredbench_amd/csrc; rebuild it"
+                )
+        try:
+            handle = ctypes.CDLL(str(lib_path))
+        except OSError as exc:
+            raise NativeLibraryError(f"cannot load {lib_path}: {exc}") from exc
+        bind(handle)
+        version = handle.mb_abi_version()
+        if version != ABI_VERSION:
+            raise NativeLibraryError(f"{lib_path} has ABI version {version}, expected {ABI_VERSION}")
+        lib = NativeLibrary(path=lib_path, handle=handle)
+        _cache[lib_path] = lib
+        return lib

@@ -1,0 +1,81 @@
+"""Torch-backend helpers (src/teamredbench/utils.py:14-48) plus seeded inputs.
+
+``timed_iterations`` is the reference's wall-clock mean between device
+synchronisations. The native backend times with hipEvents inside the
+library instead (mb_time_stream / mb_time_gemm).
+"""
+from __future__ import annotations
+
+import math
+import time
+from typing import Any, Callable
+
+from teamredbench_amd.device import synchronize_rocm_device
+from teamredbench_amd.dtypes import DTypeSpec
+
+
+def synchronize(torch_module: Any) -> None:
+    synchronize_rocm_device(torch_module)
+
+
+def timed_iterations(fn: Callable[[], None], *, torch_module: Any, warmup: int, iterations: int) -> float:
+    for _ in range(warmup):
+        fn()
+    synchronize(torch_module)
+    start = time.perf_counter()
+    for _ in range(iterations):
+        fn()
+    synchronize(torch_module)
+    return (time.perf_counter() - start) / max(iterations, 1)
+
+
+def make_tensor(torch_module: Any, spec: DTypeSpec, shape: tuple[int, ...], device: Any):
+    """Unseeded random tensor of `spec` (the reference torch backend's inputs)."""
+    torch = torch_module
+    dtype = getattr(torch, spec.torch_attr)
+    if spec.kind == "bool":
+        return torch.randint(0, 2, shape, device=device, dtype=torch.uint8).to(dtype=dtype)
+    if spec.kind == "integer":
+        return torch.randint(0, 17, shape, device=device, dtype=dtype)
+    if spec.kind == "complex":
+        real_dtype = torch.float32 if spec.name == "complex64" else torch.float64
+        return torch.complex(
+            torch.randn(shape, device=device, dtype=real_dtype),
+            torch.randn(shape, device=device, dtype=real_dtype),
+        ).to(dtype=dtype)
+    return torch.randn(shape, device=device, dtype=torch.float32).to(dtype=dtype)
+
+
+def seeded_uniform(torch_module: Any, numel: int, dtype_name: str, device: Any, seed: int):
+    """uniform[-1, 1] drawn in fp32 from a device generator seeded `seed`, cast to the dtype."""
+    torch = torch_module
+    gen = torch.Generator(device=device)
+    gen.manual_seed(seed)
+    values = torch.empty(numel, device=device, dtype=torch.float32).uniform_(-1.0, 1.0, generator=gen)
+    if dtype_name == "int8":
+        return (values * 100).to(torch.int8)
+    return values.to(getattr(torch, dtype_name))
+
+
+def seeded_gemm_operands(torch_module: Any, m: int, n: int, k: int, dtype_name: str, device: Any, seed: int):
+    """GEMM operands on the device: normal(0, 1/sqrt(k)) for bf16/f16; for fp8
+    normal(0, 1) scaled per tensor so amax -> 448, cast to e4m3fn.
+    Returns (a, b, scale_a, scale_b)."""
+    torch = torch_module
+    ga = torch.Generator(device=device)
+    ga.manual_seed(seed)
+    gb = torch.Generator(device=device)
+    gb.manual_seed(seed + 1)
+    a = torch.randn(m, k, device=device, dtype=torch.float32, generator=ga)
+    b = torch.randn(k, n, device=device, dtype=torch.float32, generator=gb)
+    if dtype_name == "float8_e4m3fn":
+        sa = float(a.abs().max()) / 448.0
+        sb = float(b.abs().max()) / 448.0
+        return (a / sa).to(torch.float8_e4m3fn), (b / sb).to(torch.float8_e4m3fn), sa, sb
+    dtype = getattr(torch, dtype_name)
+    std = 1.0 / math.sqrt(k)
+    return (a * std).to(dtype), (b * std).to(dtype), 1.0, 1.0
+
+
+def tensor_nbytes(tensor: Any) -> int:
+    return int(tensor.numel() * tensor.element_size())

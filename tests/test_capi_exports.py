@@ -1,0 +1,65 @@
+"""The C-ABI library loads on a host without a GPU and exports exactly what
+include/mi355bench.h declares (no compute calls here)."""
+from __future__ import annotations
+
+import re
+import subprocess
+
+import pytest
+
+from teamredbench_amd.native import build, capi
+
+HEADER = build.PACKAGE_DIR.parent / "include" / "mi355bench.h"
+
+
+def _declared() -> set[str]:
+    text = HEADER.read_text(encoding="utf-8")
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return set(re.findall(r"\b(mb_[a-z_0-9]+)\s*\(", text))
+
+
+def test_header_declares_the_bound_signatures():
+    assert _declared() == set(capi.SIGNATURES)
+
+
+def test_library_exports_every_declared_symbol():
+    path = build.library_path()
+    assert path.exists(), "build the library first (__graft_entry__.build())"
+    out = subprocess.run(["nm", "-D", "--defined-only", str(path)], capture_output=True, text=True, check=True).stdout
+    exported = {line.split()[-1] for line in out.splitlines() if line.strip()}
+    missing = _declared() - exported
+    assert not missing, f"not exported: {sorted(missing)}"
+    # nothing else escapes under the mb_ prefix
+    assert {s for s in exported if s.startswith("mb_")} == _declared()
+
+
+def test_library_loads_and_reports_its_abi():
+    lib = capi.load_library()
+    assert lib.handle.mb_abi_version() == capi.ABI_VERSION
+    assert lib.handle.mb_last_error() == b""
+
+
+def test_stale_build_is_refused(tmp_path, monkeypatch):
+    monkeypatch.setattr(capi._build, "source_digest", lambda: "0" * 64)
+    capi._cache.clear()
+    try:
+        with pytest.raises(capi.NativeLibraryError, match="different sources"):
+            capi.load_library()
+    finally:
+        capi._cache.clear()
+
+
+def test_missing_library_is_an_error_not_a_fallback(tmp_path):
+    with pytest.raises(capi.NativeLibraryError, match="not built"):
+        capi.load_library(tmp_path / "libmissing.so")
+
+
+def test_abi_constants_match_the_header():
+    text = HEADER.read_text(encoding="utf-8")
+    consts = dict(re.findall(r"#define (MB_[A-Z0-9_]+) (-?\d+)", text))
+    assert int(consts["MB_ABI_VERSION"]) == capi.ABI_VERSION
+    assert int(consts["MB_OP_TRIAD"]) == capi.OP_TRIAD and int(consts["MB_OP_SCALE"]) == capi.OP_SCALE
+    for name, value in capi.DTYPES.items():
+        assert int(consts["MB_DT_" + name.upper()]) == value
+    assert int(consts["MB_ERR_SHAPE"]) == capi.MB_ERR_SHAPE
+    assert int(consts["MB_ERR_WORKSPACE"]) == capi.MB_ERR_WORKSPACE
