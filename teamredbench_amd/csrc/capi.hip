@@ -277,6 +277,7 @@ int mb_kernel_info(int kind, int a, int b, int64_t m, int64_t n, int64_t k, char
         j.num("vector_unroll", plan.chunks_per_trip);
         j.num("blocks_per_cu", plan.blocks_per_cu);
         j.num("grid_blocks", plan.blocks);
+        j.str("schedule", plan.span ? "block_span" : "grid_stride");
         j.num("vector_bytes", 16);
         j.boolean("nontemporal", plan.nontemporal);
         j.str("arch", props->arch);

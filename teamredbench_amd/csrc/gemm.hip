@@ -2,11 +2,12 @@
 // forwards the launch. Validation of dtype and sizes lives here.
 #include "gemm_common.hpp"
 
+#include <cstdlib>
+
 namespace mb {
 
 int gemm_plan(int dtype, int64_t M, int64_t N, int64_t K, const DeviceProps& props,
               GemmPlan* plan) {
-    (void)props;
     if (dtype != MB_DT_BFLOAT16 && dtype != MB_DT_FLOAT16 && dtype != MB_DT_FLOAT8_E4M3FN) {
         set_error("GEMM supports bfloat16, float16 and float8_e4m3fn (got %s)", dtype_name(dtype));
         return MB_ERR_UNSUPPORTED;
@@ -16,6 +17,9 @@ int gemm_plan(int dtype, int64_t M, int64_t N, int64_t K, const DeviceProps& pro
                   (long long)K);
         return MB_ERR_INVALID_ARG;
     }
+    if (std::getenv("MB_GEMM_FORCE_GENERIC") == nullptr &&
+        gemm_tiled_plan(dtype, M, N, K, props, plan) == MB_OK)
+        return MB_OK;
     return gemm_generic_plan(dtype, M, N, K, plan);
 }
 
@@ -27,6 +31,8 @@ int gemm_launch(int dtype, const void* A, const void* B, void* C, int64_t M, int
     switch (plan.variant) {
         case kVariantGeneric:
             return gemm_generic_launch(dtype, A, B, C, M, N, K, alpha, stream);
+        case kVariantTiled:
+            return gemm_tiled_launch(dtype, A, B, C, M, N, K, alpha, plan, stream);
         default:
             set_error("GEMM plan variant %d not available", plan.variant);
             return MB_ERR_UNSUPPORTED;

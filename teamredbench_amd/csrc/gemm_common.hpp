@@ -58,6 +58,10 @@ __device__ inline void store_out(void* C, int64_t idx, float v) {
 }
 
 int gemm_generic_plan(int dtype, int64_t M, int64_t N, int64_t K, GemmPlan* plan);
+int gemm_tiled_plan(int dtype, int64_t M, int64_t N, int64_t K, const DeviceProps& props,
+                    GemmPlan* plan);
+int gemm_tiled_launch(int dtype, const void* A, const void* B, void* C, int64_t M, int64_t N,
+                      int64_t K, float alpha, const GemmPlan& plan, hipStream_t stream);
 int gemm_generic_launch(int dtype, const void* A, const void* B, void* C, int64_t M, int64_t N,
                         int64_t K, float alpha, hipStream_t stream);
 

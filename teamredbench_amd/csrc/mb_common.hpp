@@ -91,6 +91,7 @@ struct StreamPlan {
     bool nontemporal = false;
     uint64_t chunks = 0;        // 16-byte chunks in the vector body
     uint64_t tail = 0;          // elements after the vector body
+    uint64_t span = 0;          // chunks per block (0 = grid-stride schedule)
 };
 
 int stream_plan(int op, int dtype, const void* dst, const void* b, const void* c,
@@ -111,6 +112,7 @@ struct GemmPlan {
     int tile_group_m = 0;
     size_t workspace = 0;
     int variant = 0;            // kernel family selector, private to gemm*.hip
+    int config = 0;             // configuration within the family
 };
 
 int gemm_plan(int dtype, int64_t M, int64_t N, int64_t K, const DeviceProps& props,

@@ -218,18 +218,30 @@ __device__ inline void store_chunk(u32x4* p, u32x4 v) {
 
 // Vector body over `chunks` 16-byte chunks, then the `tail` trailing elements
 // (fewer than one chunk) handled by the first threads of the grid.
+// span == 0: grid-stride -- consecutive trips of a thread are one grid apart.
+// span  > 0: each block walks its own contiguous run of `span` chunks, the
+//            block's lanes side by side, trips one block-width apart.
 template <int OP, int DT, int U, bool NT>
-__global__ void __launch_bounds__(256)
+__global__ void __launch_bounds__(1024)
 stream_vec_kernel(void* __restrict__ dst, const void* __restrict__ b, const void* __restrict__ c,
-                  uint64_t chunks, uint64_t tail, float s, double sd) {
+                  uint64_t chunks, uint64_t tail, uint64_t span, float s, double sd) {
     const u32x4* B = static_cast<const u32x4*>(b);
     const u32x4* C = static_cast<const u32x4*>(c);
     u32x4* D = static_cast<u32x4*>(dst);
-    const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
     const uint64_t tid = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    uint64_t i = tid;
+    uint64_t stride, end, i;
+    if (span == 0) {
+        stride = (uint64_t)gridDim.x * blockDim.x;
+        end = chunks;
+        i = tid;
+    } else {
+        stride = blockDim.x;
+        const uint64_t first = (uint64_t)blockIdx.x * span;
+        end = first + span < chunks ? first + span : chunks;
+        i = first + threadIdx.x;
+    }
     // Full trips: all U chunks of this thread are in range.
-    for (; i + (U - 1) * stride < chunks; i += U * stride) {
+    for (; i + (U - 1) * stride < end; i += U * stride) {
         u32x4 vb[U];
         u32x4 vc[U];
 #pragma unroll
@@ -243,7 +255,7 @@ stream_vec_kernel(void* __restrict__ dst, const void* __restrict__ b, const void
             store_chunk<NT>(D + i + u * stride, ChunkOp<OP, DT>::apply(vb[u], vc[u], s, sd));
     }
     // Remainder trip: fewer than U chunks left for this thread.
-    for (; i < chunks; i += stride) {
+    for (; i < end; i += stride) {
         u32x4 vb = load_chunk<NT>(B + i);
         u32x4 vc = vb;
         if (OP == MB_OP_TRIAD) vc = load_chunk<NT>(C + i);
@@ -258,7 +270,7 @@ stream_vec_kernel(void* __restrict__ dst, const void* __restrict__ b, const void
 
 // Element-wise grid-stride kernel for buffers that are not 16-byte aligned.
 template <int OP, int DT>
-__global__ void __launch_bounds__(256)
+__global__ void __launch_bounds__(1024)
 stream_scalar_kernel(void* __restrict__ dst, const void* __restrict__ b, const void* __restrict__ c,
                      uint64_t n, float s, double sd) {
     const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
@@ -268,7 +280,7 @@ stream_scalar_kernel(void* __restrict__ dst, const void* __restrict__ b, const v
 
 // ---- dispatch --------------------------------------------------------------
 
-typedef void (*VecKernel)(void*, const void*, const void*, uint64_t, uint64_t, float, double);
+typedef void (*VecKernel)(void*, const void*, const void*, uint64_t, uint64_t, uint64_t, float, double);
 typedef void (*ScalarKernel)(void*, const void*, const void*, uint64_t, float, double);
 
 template <int OP, int DT>
@@ -332,20 +344,27 @@ ScalarKernel scalar_kernel_for(int op, int dtype) {
     return nullptr;
 }
 
-// Tuned defaults: blocks of 256 threads per CU and 16-byte chunks per thread
-// per trip, per (op, dtype). Environment overrides exist for sweeps:
-// MB_STREAM_UNROLL (1,2,4,8), MB_STREAM_NT (0/1), MB_STREAM_THREADS (64..1024
-// multiple of 64; 256 max for the launch bound).
+// Tuned defaults per (op, dtype): blocks per CU, threads per block, 16-byte
+// chunks per thread per trip, nontemporal hint and schedule (0 grid-stride,
+// 1 contiguous span per block). Environment overrides exist for sweeps:
+// MB_STREAM_UNROLL (1,2,4,8), MB_STREAM_NT (0/1), MB_STREAM_THREADS (64..1024,
+// multiple of 64), MB_STREAM_SCHED (0/1).
 struct StreamTuning {
     int blocks_per_cu;
+    int threads;
     int unroll;
     bool nontemporal;
+    int schedule;
 };
 
+// Measured on MI355X at 2^28 fp32 elements: one 256-thread block per CU with
+// nontemporal accesses beats deeper occupancy (more requests in flight spread
+// over more DRAM pages); triad (two read streams) prefers 2 chunks per trip,
+// copy and scale (one read stream) 4.
 StreamTuning default_tuning(int op, int dtype) {
     (void)dtype;
-    if (op == MB_OP_TRIAD) return {8, 4, true};
-    return {8, 4, true};
+    if (op == MB_OP_TRIAD) return {1, 256, 2, true, 0};
+    return {1, 256, 4, true, 0};
 }
 
 int env_int(const char* name, int fallback) {
@@ -377,8 +396,9 @@ int stream_plan(int op, int dtype, const void* dst, const void* b, const void* c
     int u = env_int("MB_STREAM_UNROLL", t.unroll);
     if (u != 1 && u != 2 && u != 4 && u != 8) u = t.unroll;
     const bool nt = env_int("MB_STREAM_NT", t.nontemporal ? 1 : 0) != 0;
-    int threads = env_int("MB_STREAM_THREADS", 256);
-    if (threads < 64 || threads > 256 || threads % 64 != 0) threads = 256;
+    int threads = env_int("MB_STREAM_THREADS", t.threads);
+    if (threads < 64 || threads > 1024 || threads % 64 != 0) threads = t.threads;
+    const int sched = env_int("MB_STREAM_SCHED", t.schedule) == 1 ? 1 : 0;
     const int bpc = blocks_per_cu > 0 ? blocks_per_cu : t.blocks_per_cu;
 
     plan->threads = threads;
@@ -404,6 +424,16 @@ int stream_plan(int op, int dtype, const void* dst, const void* b, const void* c
     uint64_t blocks = by_work < max_blocks ? by_work : max_blocks;
     if (blocks < 1) blocks = 1;
     plan->blocks = (int)blocks;
+    plan->span = 0;
+    if (vec && sched == 1 && plan->chunks > 0) {
+        // Contiguous runs, a whole number of block-wide trips each.
+        const uint64_t trip = (uint64_t)threads * (uint64_t)u;
+        uint64_t span = (plan->chunks + blocks - 1) / blocks;
+        span = (span + trip - 1) / trip * trip;
+        plan->span = span;
+        plan->blocks = (int)((plan->chunks + span - 1) / span);
+        if ((uint64_t)plan->blocks * threads < plan->tail) plan->blocks = (int)((plan->tail + threads - 1) / threads);
+    }
     return MB_OK;
 }
 
@@ -418,7 +448,7 @@ int stream_launch(int op, int dtype, void* dst, const void* b, const void* c, ui
             return MB_ERR_UNSUPPORTED;
         }
         hipLaunchKernelGGL(k, dim3(plan.blocks), dim3(plan.threads), 0, stream, dst, b, c,
-                           plan.chunks, plan.tail, sf, s);
+                           plan.chunks, plan.tail, plan.span, sf, s);
     } else {
         ScalarKernel k = scalar_kernel_for(op, dtype);
         if (k == nullptr) {

@@ -271,5 +271,5 @@ def run_native_kernel(kernel: ResolvedNativeKernel, args: list[str], timeout_s: 
         raise NativeKernelError(f"Native kernel {kernel.name} timed out after {timeout_s} s") from exc
     if proc.returncode != 0:
         detail = proc.stderr.strip() or proc.stdout.strip() or "native kernel process failed"
-        raise NativeKernelError(f"Native kernel {kernel.name} failed: {detail}")
+        raise NativeKernelError(f"Native kernel {kernel.name} failed (exit status {proc.returncode}): {detail}")
     return parse_native_result(proc.stdout)

@@ -1,0 +1,328 @@
+"""The registry/suite/record/metric harness around the native path (CPU only).
+
+Mirrors the reference's own unit and integration tests
+(tests/test_metrics.py, test_registry.py, test_runner.py, test_native.py,
+test_autoprofile.py, test_config.py, test_profiles.py): the metric
+known-answer values are the reference's numbers, and the external-executable
+contract is driven through fake executables written by the test.
+"""
+from __future__ import annotations
+
+import json
+from pathlib import Path
+from types import SimpleNamespace
+
+import pytest
+import yaml
+
+import teamredbench_amd.builtin  # noqa: F401
+from teamredbench_amd import runner as runner_mod
+from teamredbench_amd.benchmarks.base import Benchmark, BenchmarkRecord
+from teamredbench_amd.config import load_hardware_profile, load_suite
+from teamredbench_amd.device import DeviceInfo
+from teamredbench_amd.metrics.common import (
+    achieved_tops,
+    bus_bandwidth_gbps,
+    gemm_bandwidth_gbps,
+    hbm_bandwidth_gbps,
+    hbm_efficiency_pct,
+    latency_us,
+    link_efficiency_pct,
+    mfu_pct,
+    payload_bandwidth_gbps,
+)
+from teamredbench_amd.native import runtime as native_runtime
+from teamredbench_amd.native.registry import get_native_kernel, list_native_kernels, registered_names
+from teamredbench_amd.native.runtime import ResolvedNativeKernel
+from teamredbench_amd.registry import get_benchmark, list_benchmarks, list_metrics, register_benchmark
+from teamredbench_amd.runner import run_suite
+
+PACKAGE = Path(teamredbench_amd.builtin.__file__).resolve().parent
+HW_DIR = PACKAGE / "configs" / "profiles" / "hardware"
+
+
+# ---------------------------------------------------------------- metrics
+def test_hbm_metrics_known_answers():
+    raw = {"elapsed_s": 0.5, "moved_bytes": 1_000_000_000, "peak_bandwidth_gbps": 4.0}
+    assert hbm_bandwidth_gbps(raw) == 2.0
+    assert hbm_efficiency_pct(raw) == 50.0
+    assert latency_us(raw) == 500000.0
+
+
+def test_mfu_metrics_known_answers():
+    raw = {"elapsed_s": 0.1, "achieved_ops": 5_000_000_000_000, "peak_tops": 100.0}
+    assert achieved_tops(raw) == 50.0
+    assert mfu_pct(raw) == 50.0
+
+
+def test_collective_metrics_known_answers():
+    raw = {"elapsed_s": 0.25, "payload_bytes": 500_000_000, "bus_factor": 1.5, "peak_link_bandwidth_gbps": 4.0}
+    assert payload_bandwidth_gbps(raw) == 2.0
+    assert bus_bandwidth_gbps(raw) == 3.0
+    assert link_efficiency_pct(raw) == 75.0
+
+
+def test_metrics_are_none_without_inputs():
+    assert mfu_pct({"elapsed_s": 0.001, "achieved_ops": 1e9}) is None
+    assert hbm_efficiency_pct({"elapsed_s": 0.001, "moved_bytes": 1e9, "peak_bandwidth_gbps": 0}) is None
+    assert hbm_bandwidth_gbps({"moved_bytes": 1e9}) is None
+    assert gemm_bandwidth_gbps({"elapsed_s": 2.0, "gemm_bytes": 4e9}) == 2.0
+
+
+# ---------------------------------------------------------------- registries
+def test_builtin_benchmarks_metrics_and_native_kernels():
+    assert {"hbm", "mfu"} <= set(list_benchmarks())
+    assert {"latency_us", "hbm_bandwidth_gbps", "hbm_efficiency_pct", "achieved_tops", "mfu_pct"} <= set(list_metrics())
+    # the reference's built-in kernel names resolve to the gfx950 kernels
+    assert {"hbm_hip", "mfu_hipblas", "hbm_gfx950", "mfu_gfx950"} <= registered_names()
+    assert get_native_kernel("hbm_hip").name == "hbm_gfx950"
+    assert get_native_kernel("mfu_hipblas").benchmark == "mfu"
+    assert {d.name for d in list_native_kernels()} >= {"hbm_gfx950", "mfu_gfx950"}
+
+
+# ---------------------------------------------------------------- suite plumbing
+def _write_profiles(tmp: Path, compute: dict | None = None, hbm: float = 4000) -> tuple[Path, Path]:
+    hardware, runtime = tmp / "hardware.yaml", tmp / "runtime.yaml"
+    hardware.write_text(yaml.safe_dump({
+        "name": "test-hw", "family": "cdna", "peak_hbm_bandwidth_gbps": hbm,
+        "peak_link_bandwidth_gbps": {"xgmi": 1, "network": 1},
+        "peak_compute_tops": compute if compute is not None else {"float32": 100},
+    }), encoding="utf-8")
+    runtime.write_text(yaml.safe_dump({"name": "test-runtime", "rocm_version": "test", "libraries": {}, "env": {}}),
+                       encoding="utf-8")
+    return hardware, runtime
+
+
+def _write_suite(tmp: Path, name: str, benchmarks: list, formats=("json",), compute=None, hbm=4000) -> Path:
+    hardware, runtime = _write_profiles(tmp, compute, hbm)
+    suite = tmp / "suite.yaml"
+    suite.write_text(yaml.safe_dump({
+        "name": name, "device": {"profile": str(hardware)}, "runtime": {"profile": str(runtime)},
+        "outputs": {"directory": str(tmp / "results"), "formats": list(formats)}, "benchmarks": benchmarks,
+    }), encoding="utf-8")
+    return suite
+
+
+@register_benchmark("test_dummy_callback")
+class DummyCallbackBenchmark(Benchmark):
+    default_metrics = ["latency_us", "mfu_pct"]
+
+    def run(self) -> list[BenchmarkRecord]:
+        return [self.emit_record(BenchmarkRecord(benchmark=self.name, case="single", dtype="float32",
+                                                 raw_metrics={"elapsed_s": 0.001, "achieved_ops": 1e9}))]
+
+
+def test_run_suite_invokes_record_callback_with_metrics(tmp_path: Path):
+    suite = _write_suite(tmp_path, "callback-suite", [{"benchmark": "test_dummy_callback"}], formats=("json", "csv"),
+                         compute={"float32": 1}, hbm=1)
+    seen: list[BenchmarkRecord] = []
+    summary = run_suite(suite, record_callback=seen.append)
+    assert len(summary.records) == 1 and len(seen) == 1
+    assert seen[0].metrics["latency_us"] == 1000.0
+    assert seen[0].metrics["mfu_pct"] is None          # no peak_tops in the raw metrics
+    for key in ("json", "csv", "metadata"):
+        assert summary.outputs[key].exists()
+    records = json.loads(summary.outputs["json"].read_text(encoding="utf-8"))
+    meta = json.loads(summary.outputs["metadata"].read_text(encoding="utf-8"))
+    assert records[0]["benchmark"] == "test_dummy_callback"
+    assert meta["record_count"] == 1
+    assert meta["outputs"]["json"] == str(summary.outputs["json"])
+    assert meta["run"]["configs"]["suite"]["raw"]["name"] == "callback-suite"
+    assert meta["run"]["configs"]["hardware_profile"]["raw"]["name"] == "test-hw"
+
+
+# ---------------------------------------------------------------- executable contract
+def _fake_executable(path: Path, seen: Path, payload: dict | str, exit_code: int = 0) -> None:
+    line = payload if isinstance(payload, str) else json.dumps(payload)
+    path.write_text("\n".join([
+        "#!/usr/bin/env python3",
+        "import json, sys",
+        f"open({str(seen)!r}, 'w', encoding='utf-8').write(json.dumps(sys.argv[1:]))",
+        "print('noise before the contract line')",
+        f"print({line!r})",
+        f"sys.exit({exit_code})",
+    ]), encoding="utf-8")
+    path.chmod(0o755)
+
+
+def test_hbm_native_backend_runs_an_external_binary(tmp_path: Path):
+    seen = tmp_path / "args.json"
+    _fake_executable(tmp_path / "fake_hbm.py", seen,
+                     {"status": "ok", "raw_metrics": {"elapsed_s": 0.002}, "metadata": {"executor": "fake"}})
+    suite = _write_suite(tmp_path, "native-hbm", [{"benchmark": "hbm", "params": {
+        "backend": "native", "dtypes": ["float32"], "modes": ["copy"], "size_mib": 1024, "warmup": 2,
+        "iterations": 5, "native": {"binary": "./fake_hbm.py"}}}])
+    record = run_suite(suite).records[0]
+    assert record.status == "ok" and record.metadata["executor"] == "fake"
+    assert record.metrics["hbm_bandwidth_gbps"] == pytest.approx(1073.741824)
+    assert record.metrics["hbm_efficiency_pct"] == pytest.approx(26.8435456)
+    argv = json.loads(seen.read_text(encoding="utf-8"))
+    for token in ("--dtype", "float32", "--mode", "copy", "--size-mib", "1024", "--warmup", "2", "--iterations", "5"):
+        assert token in argv
+
+
+def test_mfu_native_backend_runs_an_external_binary(tmp_path: Path):
+    seen = tmp_path / "args.json"
+    _fake_executable(tmp_path / "fake_mfu.py", seen,
+                     {"status": "ok", "raw_metrics": {"elapsed_s": 0.001}, "metadata": {"executor": "fake"}})
+    suite = _write_suite(tmp_path, "native-mfu", [{"benchmark": "mfu", "params": {
+        "backend": "native", "dtypes": ["float32"], "shapes": [[1024, 1024, 1024]], "warmup": 2, "iterations": 5,
+        "native": {"binary": "./fake_mfu.py"}}}], compute={"float32": 20})
+    record = run_suite(suite).records[0]
+    assert record.status == "ok"
+    assert record.metrics["achieved_tops"] == pytest.approx(2.147483648)
+    assert record.metrics["mfu_pct"] == pytest.approx(10.73741824)
+    argv = json.loads(seen.read_text(encoding="utf-8"))
+    for flag in ("--m", "--n", "--k", "--dtype"):
+        assert flag in argv
+    assert argv.count("1024") == 3
+
+
+@pytest.mark.parametrize("payload, code, error", [
+    ({"status": "ok", "raw_metrics": {"elapsed_s": 0.001}}, 3, "exit"),
+    ("this is not json", 0, "JSON"),
+    ({"status": "skipped", "error": "unsupported dtype"}, 0, "unsupported dtype"),
+    ({"status": "ok", "raw_metrics": {}}, 0, "elapsed_s"),
+])
+def test_executable_failures_become_skipped_records(tmp_path: Path, payload, code, error):
+    _fake_executable(tmp_path / "fake.py", tmp_path / "args.json", payload, exit_code=code)
+    suite = _write_suite(tmp_path, "failing", [{"benchmark": "hbm", "params": {
+        "backend": "native", "dtypes": ["float32"], "modes": ["copy", "triad"], "size_mib": 1,
+        "native": {"binary": "./fake.py"}}}])
+    records = run_suite(suite).records
+    assert len(records) == 2
+    for record in records:
+        assert record.status == "skipped"
+        assert error.lower() in (record.error or "").lower()
+        assert record.metrics == {}
+
+
+def test_elapsed_seconds_alias_is_accepted(tmp_path: Path):
+    _fake_executable(tmp_path / "fake.py", tmp_path / "args.json",
+                     {"status": "ok", "raw_metrics": {"elapsed_seconds": 0.5, "moved_bytes": 1e9}})
+    suite = _write_suite(tmp_path, "alias", [{"benchmark": "hbm", "params": {
+        "backend": "native", "dtypes": ["float32"], "modes": ["copy"], "size_mib": 1,
+        "native": {"binary": "./fake.py"}}}])
+    record = run_suite(suite).records[0]
+    assert record.status == "ok" and record.metrics["hbm_bandwidth_gbps"] == 2.0
+
+
+def test_missing_binary_skips_every_case(tmp_path: Path):
+    suite = _write_suite(tmp_path, "missing", [{"benchmark": "mfu", "params": {
+        "backend": "native", "dtypes": ["float32"], "shapes": [[64, 64, 64], [128, 128, 128]],
+        "native": {"binary": "./does_not_exist"}}}], compute={"float32": 1})
+    records = run_suite(suite).records
+    assert [r.status for r in records] == ["skipped", "skipped"]
+
+
+def test_mfu_gates_dtypes_without_a_peak(tmp_path: Path):
+    _fake_executable(tmp_path / "fake.py", tmp_path / "args.json",
+                     {"status": "ok", "raw_metrics": {"elapsed_s": 0.001}})
+    suite = _write_suite(tmp_path, "gate", [{"benchmark": "mfu", "params": {
+        "backend": "native", "dtypes": ["float16"], "shapes": [[64, 64, 64]],
+        "native": {"binary": "./fake.py"}}}], compute={"float32": 1})
+    record = run_suite(suite).records[0]
+    assert record.status == "skipped" and "peak" in record.error.lower()
+
+
+# ---------------------------------------------------------------- built-in C-ABI kernels on a host without a GPU
+class _TorchWithoutDevice:
+    """The real torch module with no visible GPU."""
+
+    def __init__(self):
+        import torch
+
+        self._torch = torch
+        self.cuda = SimpleNamespace(is_available=lambda: False)
+
+    def __getattr__(self, name):
+        return getattr(self._torch, name)
+
+
+def test_builtin_kernels_skip_cleanly_without_a_device(tmp_path: Path, monkeypatch):
+    monkeypatch.setattr(runner_mod, "load_torch", _TorchWithoutDevice)
+    suite = _write_suite(tmp_path, "builtin", [
+        {"benchmark": "hbm", "params": {"backend": "native", "dtypes": ["float32"], "modes": ["copy", "triad"],
+                                        "size_mib": 1}},
+        {"benchmark": "mfu", "params": {"backend": "native", "dtypes": ["float32"], "shapes": [[64, 64, 64]]}},
+    ], compute={"float32": 1})
+    records = run_suite(suite).records
+    assert len(records) == 3
+    assert all(r.status == "skipped" for r in records)
+    assert all(r.metadata.get("kernel") in ("hbm_gfx950", "mfu_gfx950") for r in records)
+
+
+# ---------------------------------------------------------------- native cache
+def test_prepare_native_kernel_binary_rebuilds_when_local_include_changes(tmp_path: Path, monkeypatch):
+    source, include = tmp_path / "kernel.hip.cpp", tmp_path / "kernel_impl.hip.hpp"
+    source.write_text('#include "kernel_impl.hip.hpp"\nint main() { return kValue; }\n', encoding="utf-8")
+    include.write_text("static constexpr int kValue = 0;\n", encoding="utf-8")
+    monkeypatch.setattr(native_runtime, "_find_hip_compiler", lambda preferred=None: "/opt/rocm/bin/hipcc")
+    outputs: list[Path] = []
+
+    def fake_run(command, **_):
+        out = Path(command[command.index("-o") + 1])
+        out.write_text("fake-binary", encoding="utf-8")
+        outputs.append(out)
+        return SimpleNamespace(returncode=0, stderr="", stdout="")
+
+    monkeypatch.setattr(native_runtime.subprocess, "run", fake_run)
+    kernel = ResolvedNativeKernel(benchmark="mfu", name="unit-test-kernel", description="cache test",
+                                  source_path=source, cache_dir=tmp_path / "cache")
+    first = native_runtime.prepare_native_kernel_binary(kernel)
+    assert native_runtime.prepare_native_kernel_binary(kernel) == first and len(outputs) == 1  # cached
+    include.write_text("static constexpr int kValue = 1;\n", encoding="utf-8")
+    second = native_runtime.prepare_native_kernel_binary(kernel)
+    assert first != second and outputs == [first, second]
+
+
+def test_clean_native_cache_command_removes_entries(tmp_path: Path):
+    from typer.testing import CliRunner
+
+    from teamredbench_amd.cli import app
+
+    cache = tmp_path / "native-cache"
+    cache.mkdir()
+    (cache / "kernel-a").write_text("a", encoding="utf-8")
+    (cache / "kernel-b").mkdir()
+    (cache / "kernel-b" / "payload").write_text("b", encoding="utf-8")
+    result = CliRunner().invoke(app, ["clean-native-cache", "--cache-dir", str(cache)])
+    assert result.exit_code == 0
+    assert f"Native cache: {cache}" in result.stdout and "Removed entries: 2" in result.stdout
+    assert list(cache.iterdir()) == []
+
+
+def test_cli_lists_native_kernels():
+    from typer.testing import CliRunner
+
+    from teamredbench_amd.cli import app
+
+    result = CliRunner().invoke(app, ["list-native-kernels"])
+    assert result.exit_code == 0 and "hbm_gfx950" in result.stdout and "mfu_gfx950" in result.stdout
+
+
+# ---------------------------------------------------------------- profiles
+def test_mi355x_profile_peaks():
+    profile = load_hardware_profile(HW_DIR / "amd_instinct_mi355x.yaml")
+    assert profile.peak_hbm_bandwidth_gbps == 8000.0
+    assert profile.peak_compute_tops["bfloat16"] == 2500.0
+    assert profile.peak_compute_tops["float16"] == 2500.0
+    assert profile.peak_compute_tops["float8_e4m3fn"] == 5000.0
+
+
+def test_packaged_suites_load():
+    for suite_path in sorted((PACKAGE / "configs" / "suites").glob("*.yaml")):
+        suite = load_suite(suite_path)
+        assert suite.benchmarks, suite_path
+        for inv in suite.benchmarks:
+            assert get_benchmark(inv.benchmark)
+
+
+def test_generic_profile_is_replaced_by_the_detected_sku(monkeypatch):
+    monkeypatch.setattr(runner_mod, "load_torch", lambda: object())
+    monkeypatch.setattr(runner_mod, "detect_device",
+                        lambda torch_module, device_id=0: DeviceInfo(index=0, name="AMD Instinct MI355X"))
+    suite = load_suite(PACKAGE / "configs" / "suites" / "native_smoke.yaml")
+    context, note = runner_mod.build_context(suite)
+    assert context.hardware_profile.name == "amd-instinct-mi355x"
+    assert note and "Auto-selected" in note
