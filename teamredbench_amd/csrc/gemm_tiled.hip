@@ -1,56 +1,92 @@
-// LDS-tiled MFMA GEMM for gfx950: C = alpha * (A * B), A (M x K) and B (K x N)
-// row-major, fp32 accumulation, output bf16 (bf16 and fp8 e4m3 inputs) or
-// fp16 (fp16 inputs). Takes shapes with M % BM == 0, N % BN == 0 and
-// K % BK == 0; everything else goes to the generic kernel.
+// LDS-pipelined MFMA GEMM for gfx950: C = alpha * (A * B), A (M x K) and
+// B (K x N) row-major, fp32 accumulation, output bf16 (bf16 and fp8 e4m3
+// inputs) or fp16 (fp16 inputs). Takes shapes with M % BM == 0,
+// N % BN == 0 and K a multiple of the stage depth; everything else goes to
+// the generic kernel.
 //
-// Block tile BM x BN, K step of 128 bytes per row (BK = 64 for 16-bit
-// inputs, 128 for fp8). Both operands live in LDS K-contiguous -- A as
-// [m][128 B], B as [n][128 B] -- so every lane fetches its MFMA operand with
-// one (16-bit) or two (fp8) 16-byte LDS reads. B arrives N-contiguous from
-// HBM: each thread loads an 8-column strip of 8 (16-bit) or 16 (fp8) K-rows
-// and transposes it in registers before the LDS write, so no re-layout pass
-// over B runs outside the kernel. 16-byte chunks are XOR-swizzled by row
-// (chunk ^ ((row ^ row >> 3) & 7)), which keeps the MFMA operand reads and
-// the A writes free of bank conflicts.
+// Data path. Every stage holds 64 bytes of K per row: A as [BM rows][64 B],
+// B as [K rows][BN * elem bytes] -- B keeps its HBM layout (N-contiguous).
+// Both arrive with buffer_load_dwordx4 ... lds (HBM/L2 -> LDS, no register
+// staging): one wave instruction fills 1 KiB of LDS in lane order, and each
+// lane picks the global 16 bytes that belong at its slot of the swizzled
+// layout. The MFMA operands come out of LDS with ds_read_b128 for A and the
+// gfx950 transposing reads (ds_read_b64_tr_b16 for 16-bit B,
+// ds_read_b64_tr_b8 for fp8 B), which hand each lane 4 (8) consecutive K
+// values of one B column -- the MFMA operand layout -- with no transpose pass
+// anywhere.
 //
-// Two LDS buffers: while the waves run the MFMAs of step k out of one
-// buffer, the buffer loads of step k+1 are in flight into registers; they go
-// to the other buffer after the MFMAs, and one barrier per step orders both.
-// The K loop is unrolled by two so every LDS address is a loop-invariant
-// register plus an immediate.
+// LDS swizzles (16-byte chunk c of a row is stored at chunk c ^ f(row)):
+//   A rows (4 chunks):          f = ((r >> 1) & 3) ^ ((r >> 3) & 1)
+//   16-bit B rows (32 chunks):  f = ((k << 2) ^ (k << 1)) & 15, k = row & 3
+//   fp8 B rows (16 chunks):     f = (2k) ^ (k >> 2),            k = row & 7
+// Each keeps every operand read of a wave free of bank conflicts for both 8-
+// and 16-lane LDS phases (checked exhaustively on the host).
 //
-// Waves form a WGM x WGN grid; each wave owns a (BM/WGM) x (BN/WGN) block of
-// 32 x 32 fragments: v_mfma_f32_32x32x16_{bf16,f16}, or for fp8
-// v_mfma_f32_32x32x64_f8f6f4 (e4m3 operands). The MFMA takes the B fragment
-// as its first operand, so a lane's 16 accumulators are 4 runs of 4
+// Pipeline. STAGES LDS slots form a ring; the loads of step k + STAGES - 1
+// are issued as soon as every wave has finished step k - 1 (one barrier per
+// step), so STAGES - 1 steps of loads are in flight under the MFMAs. The
+// barrier is a bare s_barrier preceded by an explicit vmcnt wait for this
+// step's own loads only -- a full __syncthreads() would wait for all of them.
+//
+// Waves form a WGM x WGN grid; each wave owns (BM/WGM) x (BN/WGN) of C as
+// 32 x 32 fragments: v_mfma_f32_32x32x16_{bf16,f16} (two per stage), or for
+// fp8 v_mfma_f32_32x32x64_f8f6f4 (one per stage). The MFMA takes the B
+// fragment as its first operand, so a lane's 16 accumulators are 4 runs of 4
 // consecutive C columns in one C row: the epilogue stores 8 bytes at a time.
 //
-// Tile order: blocks are dispatched round-robin over the 8 XCDs, so block b
-// runs on XCD b % 8; the kernel hands each XCD a contiguous range of tiles,
-// walked in groups of `group_m` tile rows so the blocks sharing an XCD's L2
-// also share A row panels and B column panels.
+// Tile order: blocks are dispatched round-robin over the 8 XCDs (block b on
+// XCD b % 8); each XCD gets a contiguous range of tiles in an order grouped
+// by `group_m` tile rows, i.e. a compact group_m x (range / group_m) patch of
+// C whose A row panels and B column panels its L2 shares.
 #include "gemm_common.hpp"
 
 #include <cstdlib>
+#include <utility>
 
 namespace mb {
 namespace {
 
-constexpr int kRowBytes = 128;  // bytes of K per LDS row (8 chunks of 16 B)
-constexpr int kBufferFlags = 0x00020000;  // raw buffer resource word 3 on gfx9
+#define MB_LDS __attribute__((address_space(3)))
 
-__device__ __forceinline__ int swz(int row) { return (row ^ (row >> 3)) & 7; }
-__device__ __forceinline__ int lds_off(int row, int chunk) {
-    return row * kRowBytes + ((chunk ^ swz(row)) << 4);
+constexpr int kStageK = 64;                  // bytes of K per row per stage
+constexpr int kBufferFlags = 0x00020000;     // raw buffer resource word 3 on gfx9
+
+__device__ __forceinline__ int swz_a(int r) { return ((r >> 1) & 3) ^ ((r >> 3) & 1); }
+__device__ __forceinline__ int swz_b16(int k) { return ((k << 2) ^ (k << 1)) & 15; }
+__device__ __forceinline__ int swz_b8(int k) { return (2 * k) ^ (k >> 2); }
+
+// Wait until at most N vector-memory operations of this wave are pending and
+// its LDS operations have drained, then join the workgroup barrier. The empty
+// asm with a memory clobber keeps the compiler from moving LDS accesses
+// across the barrier (the barrier builtin alone does not order memory).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt_and_barrier() {
+    static_assert(N >= 0 && N < 64, "vmcnt is a 6-bit counter");
+    // gfx9 s_waitcnt encoding: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt[5:4] at [15:14]
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0x0 << 8));
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
 }
 
-typedef unsigned short u16x8 __attribute__((ext_vector_type(8)));
-typedef unsigned short u16x4 __attribute__((ext_vector_type(4)));
-typedef unsigned char u8x8 __attribute__((ext_vector_type(8)));
-typedef unsigned char u8x16 __attribute__((ext_vector_type(16)));
-typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+// One LDS-DMA load: every lane fetches 16 bytes at rsrc + voff + soff and the
+// wave writes them to LDS bytes [lds_addr, lds_addr + 1024) in lane order.
+// Issued as inline asm so the compiler's wait insertion, which cannot tell
+// which ring slot the write lands in, does not put a full vmcnt drain in
+// front of every later LDS read; the callers order these loads themselves.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void lds_dma16(__amdgpu_buffer_rsrc_t rsrc, unsigned lds_addr, int voff, int soff) {
+    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+                 :
+                 : "s"(lds_addr), "v"(voff), "s"(rsrc), "s"(soff)
+                 : "memory", "m0");
+}
+#pragma clang diagnostic pop
 
-// ---- per-dtype pieces -------------------------------------------------------
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x4_t __attribute__((__vector_size__(4 * sizeof(__bf16))));
+typedef int i32x2_t __attribute__((__vector_size__(2 * sizeof(int))));
 
 template <int DT>
 struct Traits;
@@ -58,10 +94,8 @@ struct Traits;
 template <>
 struct Traits<MB_DT_BFLOAT16> {
     static constexpr int kElem = 2;
-    static constexpr int kBK = 64;          // K elements per step
-    static constexpr int kStripRows = 8;    // K rows per B strip (16-byte row loads)
-    static constexpr int kSub = 4;          // MFMA K substeps per step
-    typedef u32x4 Frag;                     // one lane's operand: 8 bf16
+    static constexpr int kSub = 2;          // MFMAs per fragment pair per stage (K = 16 each)
+    typedef u32x4 Frag;
     __device__ static __forceinline__ f32x16 mfma(const Frag& a, const Frag& b, f32x16 c) {
         return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
                                                         __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
@@ -79,10 +113,8 @@ struct Traits<MB_DT_FLOAT16> : Traits<MB_DT_BFLOAT16> {
 template <>
 struct Traits<MB_DT_FLOAT8_E4M3FN> {
     static constexpr int kElem = 1;
-    static constexpr int kBK = 128;
-    static constexpr int kStripRows = 16;   // 8-byte row loads
-    static constexpr int kSub = 2;
-    typedef i32x8 Frag;                     // one lane's operand: 32 e4m3
+    static constexpr int kSub = 1;          // one 32x32x64 MFMA per fragment pair per stage
+    typedef i32x8 Frag;
     // Format code 0 = e4m3 for both operands; zero scale operands select the
     // unscaled encoding of the instruction.
     __device__ static __forceinline__ f32x16 mfma(const Frag& a, const Frag& b, f32x16 c) {
@@ -90,57 +122,54 @@ struct Traits<MB_DT_FLOAT8_E4M3FN> {
     }
 };
 
-// Registers of one B strip: kStripRows row loads of 8 columns.
+// A operand of substep s for this lane: row `row` of the stage, K elements
+// 8*(lane/32) .. +7 of the substep (16-bit) or 32*(lane/32) .. +31 (fp8).
 template <int DT>
-struct Strip;
-
-template <>
-struct Strip<MB_DT_BFLOAT16> {
-    u32x4 r[8];
-    __device__ __forceinline__ void load(__amdgpu_buffer_rsrc_t rsrc, int voff, int soff, int ldb) {
-#pragma unroll
-        for (int i = 0; i < 8; ++i)
-            r[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, voff, soff + i * ldb, 0));
-    }
-    // Column j (0..7) as 8 consecutive K values: 16 bytes.
-    __device__ __forceinline__ u32x4 column(int j) const {
-        u16x8 out;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) out[i] = __builtin_bit_cast(u16x8, r[i])[j];
-        return __builtin_bit_cast(u32x4, out);
-    }
-};
-template <>
-struct Strip<MB_DT_FLOAT16> : Strip<MB_DT_BFLOAT16> {};
-
-template <>
-struct Strip<MB_DT_FLOAT8_E4M3FN> {
-    u32x2 r[16];
-    __device__ __forceinline__ void load(__amdgpu_buffer_rsrc_t rsrc, int voff, int soff, int ldb) {
-#pragma unroll
-        for (int i = 0; i < 16; ++i)
-            r[i] = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rsrc, voff, soff + i * ldb, 0));
-    }
-    // Column j (0..7) as 16 consecutive K values: 16 bytes.
-    __device__ __forceinline__ u32x4 column(int j) const {
-        u8x16 out;
-#pragma unroll
-        for (int i = 0; i < 16; ++i) out[i] = __builtin_bit_cast(u8x8, r[i])[j];
-        return __builtin_bit_cast(u32x4, out);
-    }
-};
-
-// Operand fragment of a 32-row slab at `row0`, K substep `s`.
-template <int DT>
-__device__ __forceinline__ typename Traits<DT>::Frag load_frag(const unsigned char* lds, int row, int s,
-                                                               int half) {
+__device__ __forceinline__ typename Traits<DT>::Frag read_a(const unsigned char* st, int row, int s, int half) {
+    const unsigned char* p = st + row * kStageK;
+    const int f = swz_a(row);
     if constexpr (Traits<DT>::kElem == 2) {
-        // 32x32x16: lane holds K 8*half .. 8*half+7 of substep s -> chunk 2s + half.
-        return *reinterpret_cast<const u32x4*>(lds + lds_off(row, 2 * s + half));
+        return *reinterpret_cast<const u32x4*>(p + (((2 * s + half) ^ f) << 4));
     } else {
-        // 32x32x64: lane holds K 32*half .. 32*half+31 of substep s -> chunks 4s+2half, +1.
-        const u32x4 lo = *reinterpret_cast<const u32x4*>(lds + lds_off(row, 4 * s + 2 * half));
-        const u32x4 hi = *reinterpret_cast<const u32x4*>(lds + lds_off(row, 4 * s + 2 * half + 1));
+        const u32x4 lo = *reinterpret_cast<const u32x4*>(p + (((2 * half) ^ f) << 4));
+        const u32x4 hi = *reinterpret_cast<const u32x4*>(p + (((2 * half + 1) ^ f) << 4));
+        return __builtin_bit_cast(i32x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+    }
+}
+
+// B operand of substep s for this lane: column nb + lane % 32, the same K
+// range as read_a. `st` is the B part of the stage (rows of BN * elem bytes).
+template <int DT, int BN>
+__device__ __forceinline__ typename Traits<DT>::Frag read_b(const unsigned char* st, int nb, int s, int lane) {
+    const int g = lane >> 4, i = lane & 15;
+    if constexpr (Traits<DT>::kElem == 2) {
+        // Two transposing reads of 4 K-rows x 16 columns per 16-lane group.
+        constexpr int row_bytes = BN * 2;
+        u32x2 part[2];
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            const int k = 16 * s + 8 * (g >> 1) + 4 * t + (i >> 2);
+            const int n = nb + 16 * (g & 1) + 4 * (i & 3);
+            const int off = k * row_bytes + (((n >> 3) ^ swz_b16(k & 3)) << 4) + 8 * (i & 1);
+            const bf16x4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
+                (MB_LDS bf16x4_t*)((MB_LDS unsigned char*)st + off));
+            part[t] = __builtin_bit_cast(u32x2, v);
+        }
+        return __builtin_shufflevector(part[0], part[1], 0, 1, 2, 3);
+    } else {
+        // Four transposing reads of 8 K-rows x 16 columns per 16-lane group.
+        constexpr int row_bytes = BN;
+        u32x2 part[4];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            const int k = 32 * (g >> 1) + 8 * t + (i >> 1);
+            const int n = nb + 16 * (g & 1) + 8 * (i & 1);
+            const int off = k * row_bytes + (((n >> 4) ^ swz_b8(k & 7)) << 4) + 8 * (i & 1);
+            const i32x2_t v = __builtin_amdgcn_ds_read_tr8_b64_v2i32((MB_LDS i32x2_t*)((MB_LDS unsigned char*)st + off));
+            part[t] = __builtin_bit_cast(u32x2, v);
+        }
+        const u32x4 lo = __builtin_shufflevector(part[0], part[1], 0, 1, 2, 3);
+        const u32x4 hi = __builtin_shufflevector(part[2], part[3], 0, 1, 2, 3);
         return __builtin_bit_cast(i32x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
     }
 }
@@ -171,80 +200,86 @@ __device__ __forceinline__ void tile_coords(int b, int nblocks, int tiles_m, int
     *tn = r / rows;
 }
 
-template <int DT, int BM, int BN, int WGM, int WGN>
+template <int DT, int BM, int BN, int WGM, int WGN, int STAGES>
 __global__ void __launch_bounds__(64 * WGM * WGN)
 gemm_tiled_kernel(const unsigned char* __restrict__ A, const unsigned char* __restrict__ B,
                   unsigned char* __restrict__ C, int M, int N, int K, float alpha, int tiles_m,
                   int tiles_n, int group_m) {
     typedef Traits<DT> Tr;
     typedef typename Tr::Frag Frag;
-    constexpr int T = 64 * WGM * WGN;
+    constexpr int W = WGM * WGN;
     constexpr int E = Tr::kElem;
     constexpr int WTM = BM / WGM, WTN = BN / WGN;
     constexpr int FM = WTM / 32, FN = WTN / 32;
-    constexpr int A_CHUNKS = BM * 8 / T;          // 16-byte A chunks per thread per step
-    constexpr int B_STRIPS = (BN + T - 1) / T;    // B strips per thread per step
-    constexpr int A_BYTES = BM * kRowBytes, B_BYTES = BN * kRowBytes;
-    static_assert(BM * 8 % T == 0, "A tile must split evenly over the block");
-    static_assert(FM >= 1 && FN >= 1 && WTM % 32 == 0 && WTN % 32 == 0, "wave tile must be 32-aligned");
+    constexpr int K_ROWS = kStageK / E;                 // K elements per stage = B rows per stage
+    constexpr int A_BYTES = BM * kStageK;
+    constexpr int B_ROW = BN * E;                       // bytes per B row in LDS
+    constexpr int B_BYTES = K_ROWS * B_ROW;
+    constexpr int SLOT = A_BYTES + B_BYTES;
+    constexpr int A_INSTR = A_BYTES / 1024 / W;         // LDS-DMA instructions per wave per stage
+    constexpr int B_INSTR = B_BYTES / 1024 / W;
+    constexpr int LOADS = A_INSTR + B_INSTR;
+    static_assert(A_BYTES % (1024 * W) == 0 && B_BYTES % (1024 * W) == 0, "stage must split over the waves");
+    static_assert(B_ROW == 512 || B_ROW == 256, "B swizzle assumes 256- or 512-byte rows");
+    static_assert(WTM % 32 == 0 && WTN % 32 == 0, "wave tile must be 32-aligned");
+    static_assert(STAGES >= 3 && STAGES <= 6 && STAGES * SLOT <= 160 * 1024, "LDS ring does not fit");
 
-    __shared__ __attribute__((aligned(16))) unsigned char lds[2 * (A_BYTES + B_BYTES)];
+    // One array per ring slot, so every slot address is a compile-time choice.
+    __shared__ __attribute__((aligned(1024))) unsigned char ring0[SLOT], ring1[SLOT], ring2[SLOT];
+    __shared__ __attribute__((aligned(1024))) unsigned char ring3[STAGES > 3 ? SLOT : 1024];
+    __shared__ __attribute__((aligned(1024))) unsigned char ring4[STAGES > 4 ? SLOT : 1024];
+    __shared__ __attribute__((aligned(1024))) unsigned char ring5[STAGES > 5 ? SLOT : 1024];
+    auto slot_ptr = [&](auto idx) -> unsigned char* {
+        constexpr int i = decltype(idx)::value;
+        static_assert(i < STAGES, "slot out of range");
+        if constexpr (i == 0) return ring0;
+        else if constexpr (i == 1) return ring1;
+        else if constexpr (i == 2) return ring2;
+        else if constexpr (i == 3) return ring3;
+        else if constexpr (i == 4) return ring4;
+        else return ring5;
+    };
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int wave = tid >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave / WGN, wn = wave % WGN;
     int tm, tn;
     tile_coords(blockIdx.x, gridDim.x, tiles_m, tiles_n, group_m, &tm, &tn);
     const int lda = K * E;   // bytes per A row
     const int ldb = N * E;   // bytes per B row
 
-    // Buffer resources over this block's A row panel and B column panel.
     const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<unsigned char*>(A) + (int64_t)tm * BM * lda, (short)0, BM * lda, kBufferFlags);
     const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<unsigned char*>(B) + (int64_t)tn * BN * E, (short)0, K * ldb, kBufferFlags);
 
-    // A: thread t moves chunk (t % 8) of rows t/8 + i*(T/8).
-    const int a_row0 = tid >> 3, a_chunk = tid & 7;
-    const int a_voff = a_row0 * lda + a_chunk * 16;
-    // B: strip sb = t + i*T covers columns 8*(sb % (BN/8)) .. +7 and K chunk sb / (BN/8).
-    int b_voff[B_STRIPS], b_ng[B_STRIPS], b_kg[B_STRIPS];
+    // Global byte offsets of this lane's 16-byte pieces (stage 0); a stage
+    // advances A by kStageK bytes and B by K_ROWS rows.
+    int a_voff[A_INSTR], b_voff[B_INSTR];
 #pragma unroll
-    for (int i = 0; i < B_STRIPS; ++i) {
-        const int sb = tid + i * T;
-        b_ng[i] = sb % (BN / 8);
-        b_kg[i] = sb / (BN / 8);
-        b_voff[i] = b_kg[i] * Tr::kStripRows * ldb + b_ng[i] * 8 * E;
+    for (int q = 0; q < A_INSTR; ++q) {
+        const int lin = (wave * A_INSTR + q) * 1024 + lane * 16;   // LDS byte in the A part
+        const int row = lin / kStageK, pchunk = (lin % kStageK) >> 4;
+        a_voff[q] = row * lda + ((pchunk ^ swz_a(row)) << 4);
+    }
+#pragma unroll
+    for (int q = 0; q < B_INSTR; ++q) {
+        const int lin = (wave * B_INSTR + q) * 1024 + lane * 16;   // LDS byte in the B part
+        const int row = lin / B_ROW, pchunk = (lin % B_ROW) >> 4;
+        const int f = E == 2 ? swz_b16(row & 3) : swz_b8(row & 7);
+        b_voff[q] = row * ldb + ((pchunk ^ f) << 4);
     }
 
-    u32x4 a_reg[A_CHUNKS];
-    Strip<DT> b_reg[B_STRIPS];
-
-    auto load_step = [&](int kt) {
-        const int a_soff = kt * kRowBytes;
+    auto issue_stage = [&](int kt, unsigned char* slot) {
+        const unsigned base = (unsigned)(uintptr_t)(MB_LDS unsigned char*)slot;
+        const int a_soff = kt * kStageK;
 #pragma unroll
-        for (int i = 0; i < A_CHUNKS; ++i)
-            a_reg[i] = __builtin_bit_cast(
-                u32x4, __builtin_amdgcn_raw_buffer_load_b128(ra, a_voff, a_soff + i * (T / 8) * lda, 0));
-        const int b_soff = kt * Tr::kBK * ldb;
+        for (int q = 0; q < A_INSTR; ++q) lds_dma16(ra, base + (wave * A_INSTR + q) * 1024, a_voff[q], a_soff);
+        const int b_soff = kt * K_ROWS * ldb;
 #pragma unroll
-        for (int i = 0; i < B_STRIPS; ++i)
-            if (BN % T == 0 || tid + i * T < BN) b_reg[i].load(rb, b_voff[i], b_soff, ldb);
-    };
-    auto store_step = [&](int buf) {
-        unsigned char* la = lds + buf * (A_BYTES + B_BYTES);
-        unsigned char* lb = la + A_BYTES;
-#pragma unroll
-        for (int i = 0; i < A_CHUNKS; ++i)
-            *reinterpret_cast<u32x4*>(la + lds_off(a_row0 + i * (T / 8), a_chunk)) = a_reg[i];
-#pragma unroll
-        for (int i = 0; i < B_STRIPS; ++i) {
-            if (!(BN % T == 0 || tid + i * T < BN)) continue;
-#pragma unroll
-            for (int j = 0; j < 8; ++j)
-                *reinterpret_cast<u32x4*>(lb + lds_off(b_ng[i] * 8 + j, b_kg[i])) = b_reg[i].column(j);
-        }
+        for (int q = 0; q < B_INSTR; ++q)
+            lds_dma16(rb, base + A_BYTES + (wave * B_INSTR + q) * 1024, b_voff[q], b_soff);
     };
 
     f32x16 acc[FM][FN];
@@ -256,49 +291,51 @@ gemm_tiled_kernel(const unsigned char* __restrict__ A, const unsigned char* __re
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
     const int half = lane >> 5;
-    const int ra_row = wm * WTM + (lane & 31);
-    const int rb_row = wn * WTN + (lane & 31);
+    const int a_row = wm * WTM + (lane & 31);
+    const int b_col = wn * WTN;
 
-    auto compute_step = [&](int buf) {
-        const unsigned char* la = lds + buf * (A_BYTES + B_BYTES);
-        const unsigned char* lb = la + A_BYTES;
-        Frag fa[2][FM], fb[2][FN];
-#pragma unroll
-        for (int i = 0; i < FM; ++i) fa[0][i] = load_frag<DT>(la, ra_row + 32 * i, 0, half);
-#pragma unroll
-        for (int j = 0; j < FN; ++j) fb[0][j] = load_frag<DT>(lb, rb_row + 32 * j, 0, half);
+    auto compute_stage = [&](const unsigned char* slot) {
+        const unsigned char* sa = slot;
+        const unsigned char* sb = sa + A_BYTES;
 #pragma unroll
         for (int s = 0; s < Tr::kSub; ++s) {
-            const int cur = s & 1;
-            if (s + 1 < Tr::kSub) {
+            Frag fa[FM], fb[FN];
 #pragma unroll
-                for (int i = 0; i < FM; ++i) fa[cur ^ 1][i] = load_frag<DT>(la, ra_row + 32 * i, s + 1, half);
+            for (int j = 0; j < FN; ++j) fb[j] = read_b<DT, BN>(sb, b_col + 32 * j, s, lane);
 #pragma unroll
-                for (int j = 0; j < FN; ++j) fb[cur ^ 1][j] = load_frag<DT>(lb, rb_row + 32 * j, s + 1, half);
-            }
+            for (int i = 0; i < FM; ++i) fa[i] = read_a<DT>(sa, a_row + 32 * i, s, half);
 #pragma unroll
             for (int i = 0; i < FM; ++i)
 #pragma unroll
-                for (int j = 0; j < FN; ++j) acc[i][j] = Tr::mfma(fb[cur][j], fa[cur][i], acc[i][j]);
+                for (int j = 0; j < FN; ++j) acc[i][j] = Tr::mfma(fb[j], fa[i], acc[i][j]);
         }
     };
 
-    const int ksteps = K / Tr::kBK;
-    load_step(0);
-    store_step(0);
-    __syncthreads();
-    int kt = 0;
-    for (; kt + 2 <= ksteps; kt += 2) {
-        if (kt + 1 < ksteps) load_step(kt + 1);
-        compute_step(0);
-        if (kt + 1 < ksteps) store_step(1);
-        __syncthreads();
-        if (kt + 2 < ksteps) load_step(kt + 2);
-        compute_step(1);
-        if (kt + 2 < ksteps) store_step(0);
-        __syncthreads();
+    // Loads past the last stage re-read the last stage (in bounds, never
+    // consumed), so every step issues the same number of loads and the vmcnt
+    // bookkeeping stays uniform. The loop is unrolled by STAGES so every slot
+    // is a compile-time choice.
+    const int ksteps = K / K_ROWS;
+    const int last = ksteps - 1;
+    [&]<int... P>(std::integer_sequence<int, P...>) {
+        (issue_stage(min(P, last), slot_ptr(std::integral_constant<int, P>{})), ...);
+    }(std::make_integer_sequence<int, STAGES - 1>{});
+    // One step: stage kt sits in slot I; its loads are done once at most the
+    // loads of the STAGES - 2 younger stages remain, and the barrier extends
+    // that to every wave while also retiring every wave's reads of the slot
+    // the new loads go to (it held stage kt - 1).
+    auto step = [&](auto idx, int kt) {
+        constexpr int I = decltype(idx)::value;
+        wait_vmcnt_and_barrier<LOADS * (STAGES - 2)>();
+        issue_stage(min(kt + STAGES - 1, last), slot_ptr(std::integral_constant<int, (I + STAGES - 1) % STAGES>{}));
+        compute_stage(slot_ptr(idx));
+    };
+    for (int kt = 0; kt < ksteps; kt += STAGES) {
+        [&]<int... I>(std::integer_sequence<int, I...>) {
+            ((kt + I < ksteps ? step(std::integral_constant<int, I>{}, kt + I) : void()), ...);
+        }(std::make_integer_sequence<int, STAGES>{});
     }
-    if (kt < ksteps) compute_step(0);
+    wait_vmcnt_and_barrier<0>();
 
     // Epilogue. Accumulator register r = 4g + q of lane l holds
     // C[row = 32*i + l % 32][col = 32*j + 8g + 4*(l / 32) + q].
@@ -321,32 +358,33 @@ gemm_tiled_kernel(const unsigned char* __restrict__ A, const unsigned char* __re
 }
 
 struct TiledConfig {
-    int bm, bn, wgm, wgn;
+    int bm, bn, wgm, wgn, stages, group_m;
 };
 
 constexpr TiledConfig kConfigs[] = {
-    {256, 256, 2, 2},  // 0: large square-ish problems, 128 x 128 per wave
-    {128, 128, 2, 2},  // 1: mid-size problems, 64 x 64 per wave
+    {256, 256, 2, 2, 4, 8},  // 0: large problems, 128 x 128 per wave, 4 x 32 KiB stages
+    {128, 256, 2, 2, 6, 8},  // 1: mid-size problems, 64 x 128 per wave, 6 x 24 KiB stages
 };
+constexpr int kNumConfigs = sizeof(kConfigs) / sizeof(kConfigs[0]);
 
 template <int DT, int CFG>
 int launch_cfg(const void* A, const void* B, void* C, int64_t M, int64_t N, int64_t K, float alpha,
-               int group_m, hipStream_t stream) {
+               hipStream_t stream) {
     constexpr TiledConfig c = kConfigs[CFG];
     const int tiles_m = (int)(M / c.bm), tiles_n = (int)(N / c.bn);
-    hipLaunchKernelGGL((gemm_tiled_kernel<DT, c.bm, c.bn, c.wgm, c.wgn>), dim3(tiles_m * tiles_n),
+    hipLaunchKernelGGL((gemm_tiled_kernel<DT, c.bm, c.bn, c.wgm, c.wgn, c.stages>), dim3(tiles_m * tiles_n),
                        dim3(64 * c.wgm * c.wgn), 0, stream, static_cast<const unsigned char*>(A),
                        static_cast<const unsigned char*>(B), static_cast<unsigned char*>(C), (int)M,
-                       (int)N, (int)K, alpha, tiles_m, tiles_n, group_m);
+                       (int)N, (int)K, alpha, tiles_m, tiles_n, c.group_m);
     MB_HIP_TRY(hipGetLastError());
     return MB_OK;
 }
 
 template <int DT>
 int launch_dtype(int cfg, const void* A, const void* B, void* C, int64_t M, int64_t N, int64_t K,
-                 float alpha, int group_m, hipStream_t stream) {
-    if (cfg == 0) return launch_cfg<DT, 0>(A, B, C, M, N, K, alpha, group_m, stream);
-    return launch_cfg<DT, 1>(A, B, C, M, N, K, alpha, group_m, stream);
+                 float alpha, hipStream_t stream) {
+    if (cfg == 0) return launch_cfg<DT, 0>(A, B, C, M, N, K, alpha, stream);
+    return launch_cfg<DT, 1>(A, B, C, M, N, K, alpha, stream);
 }
 
 }  // namespace
@@ -357,8 +395,8 @@ int launch_dtype(int cfg, const void* A, const void* B, void* C, int64_t M, int6
 int gemm_tiled_plan(int dtype, int64_t M, int64_t N, int64_t K, const DeviceProps& props,
                     GemmPlan* plan) {
     const int64_t e = dtype == MB_DT_FLOAT8_E4M3FN ? 1 : 2;
-    const int64_t bk = 128 / e;
-    if (K % bk != 0) return MB_ERR_SHAPE;
+    const int64_t stage_k = kStageK / e;
+    if (K % stage_k != 0) return MB_ERR_SHAPE;
     if (K * N * e >= (int64_t(1) << 31) || 256 * K * e >= (int64_t(1) << 31) || M >= (int64_t(1) << 31))
         return MB_ERR_SHAPE;
     const int64_t cus = props.cu_count > 0 ? props.cu_count : 256;
@@ -368,7 +406,7 @@ int gemm_tiled_plan(int dtype, int64_t M, int64_t N, int64_t K, const DeviceProp
     const char* force = std::getenv("MB_GEMM_TILED_CONFIG");  // tuning/testing override
     if (force != nullptr && *force != '\0') {
         const int f = std::atoi(force);
-        if (f >= 0 && f < (int)(sizeof(kConfigs) / sizeof(kConfigs[0])) && fits(f)) cfg = f;
+        if (f >= 0 && f < kNumConfigs && fits(f)) cfg = f;
     }
     if (cfg >= 0)
         ;
@@ -380,12 +418,12 @@ int gemm_tiled_plan(int dtype, int64_t M, int64_t N, int64_t K, const DeviceProp
         cfg = 0;
     if (cfg < 0 || tiles(cfg) > INT32_MAX) return MB_ERR_SHAPE;
     const TiledConfig& c = kConfigs[cfg];
-    plan->implementation = "gfx950_mfma32_lds_tiled";
+    plan->implementation = "gfx950_mfma32_lds_dma";
     plan->threads = 64 * c.wgm * c.wgn;
     plan->grid = (int)tiles(cfg);
     plan->tile_m = c.bm;
     plan->tile_n = c.bn;
-    plan->tile_k = (int)bk;
+    plan->tile_k = (int)stage_k;
     plan->wave_grid_m = c.wgm;
     plan->wave_grid_n = c.wgn;
     plan->wave_tile_m = c.bm / c.wgm / 32;
@@ -393,9 +431,9 @@ int gemm_tiled_plan(int dtype, int64_t M, int64_t N, int64_t K, const DeviceProp
     plan->frag_m = 32;
     plan->frag_n = 32;
     plan->frag_k = dtype == MB_DT_FLOAT8_E4M3FN ? 64 : 16;
-    plan->k_stages = 2;
+    plan->k_stages = c.stages;
     plan->split_k = 1;
-    plan->tile_group_m = 4;
+    plan->tile_group_m = c.group_m;
     plan->workspace = 0;
     plan->variant = kVariantTiled;
     plan->config = cfg;
@@ -406,14 +444,11 @@ int gemm_tiled_launch(int dtype, const void* A, const void* B, void* C, int64_t 
                       int64_t K, float alpha, const GemmPlan& plan, hipStream_t stream) {
     switch (dtype) {
         case MB_DT_BFLOAT16:
-            return launch_dtype<MB_DT_BFLOAT16>(plan.config, A, B, C, M, N, K, alpha,
-                                                plan.tile_group_m, stream);
+            return launch_dtype<MB_DT_BFLOAT16>(plan.config, A, B, C, M, N, K, alpha, stream);
         case MB_DT_FLOAT16:
-            return launch_dtype<MB_DT_FLOAT16>(plan.config, A, B, C, M, N, K, alpha,
-                                               plan.tile_group_m, stream);
+            return launch_dtype<MB_DT_FLOAT16>(plan.config, A, B, C, M, N, K, alpha, stream);
         case MB_DT_FLOAT8_E4M3FN:
-            return launch_dtype<MB_DT_FLOAT8_E4M3FN>(plan.config, A, B, C, M, N, K, alpha,
-                                                     plan.tile_group_m, stream);
+            return launch_dtype<MB_DT_FLOAT8_E4M3FN>(plan.config, A, B, C, M, N, K, alpha, stream);
         default:
             set_error("tiled GEMM: unsupported dtype %d", dtype);
             return MB_ERR_UNSUPPORTED;

@@ -30,7 +30,7 @@ OFFLOAD_ARCH = "gfx950"
 HIP_FLAGS = [
     f"--offload-arch={OFFLOAD_ARCH}",
     "-O3",
-    "-std=c++17",
+    "-std=c++20",
     "-fPIC",
     "-Wall",
     "-Wno-unused-function",

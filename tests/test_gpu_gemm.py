@@ -61,14 +61,14 @@ def test_gemm_random_matches_fp32_matmul(lib, dtype, shape):
 
 @pytest.mark.parametrize("dtype", ["bfloat16", "float16", "float8_e4m3fn"])
 @pytest.mark.parametrize("config", ["0", "1"])
-@pytest.mark.parametrize("shape", [(256, 256, 128), (256, 512, 1024), (512, 256, 4096), (768, 1280, 384)])
+@pytest.mark.parametrize("shape", [(256, 256, 128), (256, 512, 64), (256, 512, 1024), (512, 256, 4096), (768, 1280, 384)])
 def test_tiled_configurations(lib, dtype, config, shape, monkeypatch):
     # Every tiled configuration on shapes it divides, selected through the
     # configuration override; the plan names the kernel that ran.
     monkeypatch.setenv("MB_GEMM_TILED_CONFIG", config)
     m, n, k = shape
     info = lib.gemm_info(capi.DTYPES[dtype], m, n, k)
-    assert info["implementation"] == "gfx950_mfma32_lds_tiled"
+    assert info["implementation"] == "gfx950_mfma32_lds_dma"
     assert info["tile_m"] == (256 if config == "0" else 128)
     print(f"[gemm] tiled cfg {config} {dtype} {shape}", flush=True)
     _check_random(lib, dtype, m, n, k, seed=k)
@@ -78,7 +78,7 @@ def test_tiled_configurations(lib, dtype, config, shape, monkeypatch):
 def test_large_square_takes_the_big_tile(lib, dtype):
     m = n = k = 4096
     info = lib.gemm_info(capi.DTYPES[dtype], m, n, k)
-    assert info["tile_m"] == 256 and info["implementation"] == "gfx950_mfma32_lds_tiled"
+    assert info["tile_m"] == 256 and info["implementation"] == "gfx950_mfma32_lds_dma"
     print(f"[gemm] {dtype} 4096^3 (rows sampled)", flush=True)
     _check_random(lib, dtype, m, n, k, rows=512)
 
