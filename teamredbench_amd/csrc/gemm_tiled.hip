@@ -22,11 +22,14 @@
 // Each keeps every operand read of a wave free of bank conflicts for both 8-
 // and 16-lane LDS phases (checked exhaustively on the host).
 //
-// Pipeline. STAGES LDS slots form a ring; the loads of step k + STAGES - 1
-// are issued as soon as every wave has finished step k - 1 (one barrier per
-// step), so STAGES - 1 steps of loads are in flight under the MFMAs. The
-// barrier is a bare s_barrier preceded by an explicit vmcnt wait for this
-// step's own loads only -- a full __syncthreads() would wait for all of them.
+// Pipeline. STAGES LDS slots form a ring with one barrier per stage; the
+// loads of stage k + STAGES - 1 go out in the middle of step k, as soon as
+// every wave has finished with the slot stage k - 1 used, so about
+// STAGES - 1.5 stages of loads are in flight under the MFMAs. Each stage's
+// MFMAs run in two halves, and the LDS reads of the next half (across the
+// barrier for the next stage) overlap the MFMAs of the current one. The
+// barrier is a bare s_barrier preceded by an explicit vmcnt wait for the one
+// stage needed next -- a full __syncthreads() would wait for all of them.
 //
 // Waves form a WGM x WGN grid; each wave owns (BM/WGM) x (BN/WGN) of C as
 // 32 x 32 fragments: v_mfma_f32_32x32x16_{bf16,f16} (two per stage), or for
@@ -222,7 +225,7 @@ gemm_tiled_kernel(const unsigned char* __restrict__ A, const unsigned char* __re
     static_assert(A_BYTES % (1024 * W) == 0 && B_BYTES % (1024 * W) == 0, "stage must split over the waves");
     static_assert(B_ROW == 512 || B_ROW == 256, "B swizzle assumes 256- or 512-byte rows");
     static_assert(WTM % 32 == 0 && WTN % 32 == 0, "wave tile must be 32-aligned");
-    static_assert(STAGES >= 3 && STAGES <= 6 && STAGES * SLOT <= 160 * 1024, "LDS ring does not fit");
+    static_assert(STAGES >= 4 && STAGES <= 6 && STAGES * SLOT <= 160 * 1024, "LDS ring does not fit");
 
     // One array per ring slot, so every slot address is a compile-time choice.
     __shared__ __attribute__((aligned(1024))) unsigned char ring0[SLOT], ring1[SLOT], ring2[SLOT];
@@ -294,23 +297,53 @@ gemm_tiled_kernel(const unsigned char* __restrict__ A, const unsigned char* __re
     const int a_row = wm * WTM + (lane & 31);
     const int b_col = wn * WTN;
 
-    auto compute_stage = [&](const unsigned char* slot) {
+    // Operands of half a stage. 16-bit: half p is K substep p (all fragments).
+    // fp8: the stage is one K substep; half p covers A fragments
+    // [p * FM/2, (p+1) * FM/2) and both halves use the B fragments read with
+    // half 0.
+    struct Ops {
+        Frag a[FM];
+        Frag b[FN];
+    };
+    constexpr int FM_HALF = Tr::kSub == 2 ? FM : FM / 2;
+    static_assert(Tr::kSub == 2 || FM % 2 == 0, "fp8 halves split the A fragments");
+    auto read_half = [&](const unsigned char* slot, auto part, Ops& o) {
+        constexpr int p = decltype(part)::value;
         const unsigned char* sa = slot;
-        const unsigned char* sb = sa + A_BYTES;
+        const unsigned char* sb = slot + A_BYTES;
+        if constexpr (Tr::kSub == 2) {
 #pragma unroll
-        for (int s = 0; s < Tr::kSub; ++s) {
-            Frag fa[FM], fb[FN];
+            for (int j = 0; j < FN; ++j) o.b[j] = read_b<DT, BN>(sb, b_col + 32 * j, p, lane);
 #pragma unroll
-            for (int j = 0; j < FN; ++j) fb[j] = read_b<DT, BN>(sb, b_col + 32 * j, s, lane);
+            for (int i = 0; i < FM; ++i) o.a[i] = read_a<DT>(sa, a_row + 32 * i, p, half);
+        } else {
+            if constexpr (p == 0) {
 #pragma unroll
-            for (int i = 0; i < FM; ++i) fa[i] = read_a<DT>(sa, a_row + 32 * i, s, half);
+                for (int j = 0; j < FN; ++j) o.b[j] = read_b<DT, BN>(sb, b_col + 32 * j, 0, lane);
+            }
 #pragma unroll
-            for (int i = 0; i < FM; ++i)
-#pragma unroll
-                for (int j = 0; j < FN; ++j) acc[i][j] = Tr::mfma(fb[j], fa[i], acc[i][j]);
+            for (int i = p * FM_HALF; i < (p + 1) * FM_HALF; ++i) o.a[i] = read_a<DT>(sa, a_row + 32 * i, 0, half);
         }
     };
+    auto mfma_half = [&](auto part, const Ops& o) {
+        constexpr int p = decltype(part)::value;
+        constexpr int i0 = Tr::kSub == 2 ? 0 : p * FM_HALF;
+#pragma unroll
+        for (int i = i0; i < i0 + FM_HALF; ++i)
+#pragma unroll
+            for (int j = 0; j < FN; ++j) acc[i][j] = Tr::mfma(o.b[j], o.a[i], acc[i][j]);
+    };
+    using Half0 = std::integral_constant<int, 0>;
+    using Half1 = std::integral_constant<int, 1>;
 
+    // Software pipeline over a ring of STAGES slots, one barrier per stage:
+    //   step kt (stage kt in slot kt % STAGES, its half-0 operands in `next`):
+    //     read half 1 of stage kt          | MFMAs of half 0 run meanwhile
+    //     wait for this wave's loads of stage kt+1, barrier
+    //     load stage kt+STAGES-1 into the slot stage kt-1 used
+    //     read half 0 of stage kt+1        | MFMAs of half 1 run meanwhile
+    // The barrier certifies stage kt+1 for every wave and that every wave is
+    // done reading slot kt-1 (those reads fed MFMAs before the barrier).
     // Loads past the last stage re-read the last stage (in bounds, never
     // consumed), so every step issues the same number of loads and the vmcnt
     // bookkeeping stays uniform. The loop is unrolled by STAGES so every slot
@@ -320,15 +353,26 @@ gemm_tiled_kernel(const unsigned char* __restrict__ A, const unsigned char* __re
     [&]<int... P>(std::integer_sequence<int, P...>) {
         (issue_stage(min(P, last), slot_ptr(std::integral_constant<int, P>{})), ...);
     }(std::make_integer_sequence<int, STAGES - 1>{});
-    // One step: stage kt sits in slot I; its loads are done once at most the
-    // loads of the STAGES - 2 younger stages remain, and the barrier extends
-    // that to every wave while also retiring every wave's reads of the slot
-    // the new loads go to (it held stage kt - 1).
+    Ops next;
+    wait_vmcnt_and_barrier<LOADS * (STAGES - 2)>();
+    read_half(slot_ptr(std::integral_constant<int, 0>{}), Half0{}, next);
+
     auto step = [&](auto idx, int kt) {
         constexpr int I = decltype(idx)::value;
-        wait_vmcnt_and_barrier<LOADS * (STAGES - 2)>();
+        // sched_barrier(0) keeps the scheduler from hoisting MFMAs above the
+        // LDS reads meant to overlap them.
+        const Ops cur0 = next;
+        Ops cur1 = cur0;  // fp8 keeps the B fragments of half 0
+        read_half(slot_ptr(idx), Half1{}, cur1);
+        __builtin_amdgcn_sched_barrier(0);
+        mfma_half(Half0{}, cur0);
+        __builtin_amdgcn_sched_barrier(0);
+        wait_vmcnt_and_barrier<LOADS * (STAGES - 3)>();
         issue_stage(min(kt + STAGES - 1, last), slot_ptr(std::integral_constant<int, (I + STAGES - 1) % STAGES>{}));
-        compute_stage(slot_ptr(idx));
+        read_half(slot_ptr(std::integral_constant<int, (I + 1) % STAGES>{}), Half0{}, next);
+        __builtin_amdgcn_sched_barrier(0);
+        mfma_half(Half1{}, cur1);
+        __builtin_amdgcn_sched_barrier(0);
     };
     for (int kt = 0; kt < ksteps; kt += STAGES) {
         [&]<int... I>(std::integer_sequence<int, I...>) {
@@ -362,7 +406,7 @@ struct TiledConfig {
 };
 
 constexpr TiledConfig kConfigs[] = {
-    {256, 256, 2, 2, 4, 8},  // 0: large problems, 128 x 128 per wave, 4 x 32 KiB stages
+    {256, 256, 2, 2, 5, 8},  // 0: large problems, 128 x 128 per wave, 5 x 32 KiB stages
     {128, 256, 2, 2, 6, 8},  // 1: mid-size problems, 64 x 128 per wave, 6 x 24 KiB stages
 };
 constexpr int kNumConfigs = sizeof(kConfigs) / sizeof(kConfigs[0]);
