@@ -1,0 +1,53 @@
+"""Launch the stream kernels a fixed number of times for counter collection.
+
+Run under ``rocprofv3 --pmc FETCH_SIZE`` (and, in a second pass,
+``--pmc WRITE_SIZE``): every launch is one dispatch whose DRAM traffic the
+counters report. The copy launches move a known number of bytes (read n*4,
+write n*4), which calibrates the counters; the triad launches are the
+workload being measured (read 2*n*4, write n*4).
+
+    python -m teamredbench_amd.profiling.stream_probe [--elements N] [--launches K]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import sys
+
+
+def main(argv: list[str] | None = None) -> int:
+    parser = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    parser.add_argument("--elements", type=int, default=1 << 28)
+    parser.add_argument("--launches", type=int, default=5)
+    args = parser.parse_args(argv)
+
+    import torch
+
+    from teamredbench_amd.native import capi
+
+    torch.cuda.set_device(0)
+    lib = capi.load_library()
+    n = args.elements
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(0)
+    b = torch.empty(n, device="cuda").uniform_(-1.0, 1.0, generator=gen)
+    c = torch.empty(n, device="cuda").uniform_(-1.0, 1.0, generator=gen)
+    a = torch.empty_like(b)
+    stream = torch.cuda.current_stream().cuda_stream
+    launched = {}
+    for name, op in (("copy", capi.OP_COPY), ("triad", capi.OP_TRIAD)):
+        for _ in range(args.launches):
+            lib.stream(op, capi.DT_FLOAT32, a.data_ptr(), b.data_ptr(), c.data_ptr(), n, 3.0, 0, stream)
+        torch.cuda.synchronize()
+        launched[name] = {
+            "launches": args.launches,
+            "algorithmic_read_bytes": (1 if name == "copy" else 2) * 4 * n,
+            "algorithmic_write_bytes": 4 * n,
+            "kernel": lib.stream_info(op, capi.DT_FLOAT32, n),
+        }
+    print(json.dumps({"elements": n, "cases": launched}), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

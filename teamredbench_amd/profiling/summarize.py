@@ -1,0 +1,145 @@
+"""Text summaries of rocprofv3 CSV output (kernel statistics and counters).
+
+    python -m teamredbench_amd.profiling.summarize stats <dir> [--top N]
+        per-kernel calls / average / total duration from *_kernel_stats.csv
+    python -m teamredbench_amd.profiling.summarize traffic --fetch <dir> --write <dir>
+            --kernel <regex> --calibrate <regex> --calibrate-read B --calibrate-write B
+            [--algorithmic-bytes B]
+        DRAM bytes per dispatch of the kernel matching --kernel, from
+        FETCH_SIZE / WRITE_SIZE (KiB per dispatch), each scaled by the factor
+        that makes the calibration kernel (a plain copy of known size) read
+        and write exactly its known bytes; prints a `traffic_bytes_per_launch:`
+        line that bench.py reads.
+
+    python -m teamredbench_amd.profiling.summarize mfma <dir> --kernel <regex> [--duration-us T]
+        SQ_VALU_MFMA_BUSY_CYCLES against GRBM_GUI_ACTIVE (summed over the
+        XCDs) for each matching kernel: the fraction of SIMD cycles the MFMA
+        units were busy, and, given the kernel's duration, the clock it ran at.
+
+The directories are rocprofv3 output directories written with `-f csv`.
+"""
+from __future__ import annotations
+
+import argparse
+import csv
+from pathlib import Path
+import re
+import sys
+
+from teamredbench_amd.profiling.builtin import parse_counters
+
+
+def _kernel_stats(directory: Path) -> list[dict[str, str]]:
+    rows: list[dict[str, str]] = []
+    for path in sorted(directory.rglob("*kernel_stats.csv")):
+        with path.open(newline="", encoding="utf-8", errors="replace") as handle:
+            rows.extend(csv.DictReader(handle))
+    return rows
+
+
+def _short(name: str, width: int = 110) -> str:
+    return name if len(name) <= width else name[: width - 3] + "..."
+
+
+def stats(directory: Path, top: int) -> str:
+    rows = _kernel_stats(directory)
+    if not rows:
+        raise SystemExit(f"no *kernel_stats.csv under {directory}")
+    rows.sort(key=lambda r: -float(r.get("TotalDurationNs", 0) or 0))
+    lines = [f"{'calls':>6} {'avg_us':>11} {'total_us':>12} {'pct':>6}  kernel"]
+    for r in rows[:top]:
+        lines.append(
+            f"{int(float(r['Calls'])):6d} {float(r['AverageNs']) / 1e3:11.2f} {float(r['TotalDurationNs']) / 1e3:12.1f}"
+            f" {float(r['Percentage']):6.2f}  {_short(r['Name'])}"
+        )
+    return "\n".join(lines)
+
+
+def _match(counters: dict[str, dict[str, float]], pattern: str, counter: str) -> tuple[str, float]:
+    rx = re.compile(pattern)
+    hits = [(k, v[counter]) for k, v in counters.items() if rx.search(k) and counter in v]
+    if len(hits) != 1:
+        raise SystemExit(f"pattern {pattern!r} matched {len(hits)} kernels with {counter}: {[h[0] for h in hits]}")
+    return hits[0]
+
+
+def traffic(fetch_dir: Path, write_dir: Path, kernel: str, calibrate: str, cal_read: float, cal_write: float,
+            algorithmic: float | None) -> str:
+    fetch = parse_counters(fetch_dir)
+    write = parse_counters(write_dir)
+    k_name, k_fetch = _match(fetch, kernel, "FETCH_SIZE")
+    _, k_write = _match(write, kernel, "WRITE_SIZE")
+    c_name, c_fetch = _match(fetch, calibrate, "FETCH_SIZE")
+    _, c_write = _match(write, calibrate, "WRITE_SIZE")
+    f_fetch = cal_read / (c_fetch * 1024.0)
+    f_write = cal_write / (c_write * 1024.0)
+    total = k_fetch * 1024.0 * f_fetch + k_write * 1024.0 * f_write
+    lines = [
+        f"kernel: {_short(k_name)}",
+        f"calibration kernel: {_short(c_name)} (known read {cal_read:.0f} B, write {cal_write:.0f} B)",
+        f"FETCH_SIZE per dispatch: kernel {k_fetch:.1f} KiB, calibration {c_fetch:.1f} KiB -> factor {f_fetch:.4f}",
+        f"WRITE_SIZE per dispatch: kernel {k_write:.1f} KiB, calibration {c_write:.1f} KiB -> factor {f_write:.4f}",
+        f"dram_read_bytes_per_launch: {k_fetch * 1024.0 * f_fetch:.0f}",
+        f"dram_write_bytes_per_launch: {k_write * 1024.0 * f_write:.0f}",
+        f"traffic_bytes_per_launch: {total:.0f}",
+    ]
+    if algorithmic:
+        lines.append(f"algorithmic_bytes_per_launch: {algorithmic:.0f} (traffic / algorithmic = {total / algorithmic:.4f})")
+    return "\n".join(lines)
+
+
+def mfma(directory: Path, kernel: str, durations_us: list[float], xcds: int, cus: int) -> str:
+    rx = re.compile(kernel)
+    counters = {k: v for k, v in parse_counters(directory).items() if rx.search(k)}
+    if not counters:
+        raise SystemExit(f"no kernel matching {kernel!r} under {directory}")
+    lines = []
+    for idx, (name, values) in enumerate(sorted(counters.items())):
+        busy, gui = values.get("SQ_VALU_MFMA_BUSY_CYCLES"), values.get("GRBM_GUI_ACTIVE")
+        lines.append(f"kernel: {_short(name)}")
+        for key in sorted(values):
+            lines.append(f"  {key}: {values[key]:.6g}")
+        if busy is not None and gui:
+            per_xcd = gui / xcds
+            lines.append(f"  mfma_busy_pct (busy / (GUI_ACTIVE/{xcds} * {cus} CUs * 4 SIMDs)): "
+                         f"{100.0 * busy / (per_xcd * cus * 4):.2f}")
+            if idx < len(durations_us):
+                lines.append(f"  clock over the dispatch (GUI_ACTIVE/{xcds} / duration): "
+                             f"{per_xcd / durations_us[idx] / 1e3:.3f} GHz")
+    return "\n".join(lines)
+
+
+def main(argv: list[str] | None = None) -> int:
+    parser = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    sub = parser.add_subparsers(dest="cmd", required=True)
+    p_stats = sub.add_parser("stats")
+    p_stats.add_argument("directory", type=Path)
+    p_stats.add_argument("--top", type=int, default=12)
+    p_tr = sub.add_parser("traffic")
+    p_tr.add_argument("--fetch", type=Path, required=True)
+    p_tr.add_argument("--write", type=Path, required=True)
+    p_tr.add_argument("--kernel", required=True)
+    p_tr.add_argument("--calibrate", required=True)
+    p_tr.add_argument("--calibrate-read", type=float, required=True)
+    p_tr.add_argument("--calibrate-write", type=float, required=True)
+    p_tr.add_argument("--algorithmic-bytes", type=float)
+    p_mfma = sub.add_parser("mfma")
+    p_mfma.add_argument("directory", type=Path)
+    p_mfma.add_argument("--kernel", required=True)
+    p_mfma.add_argument("--duration-us", type=float, nargs="*", default=[],
+                        help="average duration of each matching kernel, in name order")
+    p_mfma.add_argument("--xcds", type=int, default=8)
+    p_mfma.add_argument("--cus", type=int, default=256)
+    args = parser.parse_args(argv)
+    if args.cmd == "mfma":
+        print(mfma(args.directory, args.kernel, args.duration_us, args.xcds, args.cus))
+    elif args.cmd == "stats":
+        print(stats(args.directory, args.top))
+    else:
+        print(traffic(args.fetch, args.write, args.kernel, args.calibrate, args.calibrate_read,
+                      args.calibrate_write, args.algorithmic_bytes))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())
