@@ -26,13 +26,12 @@ int gemm_plan(int dtype, int64_t M, int64_t N, int64_t K, const DeviceProps& pro
 int gemm_launch(int dtype, const void* A, const void* B, void* C, int64_t M, int64_t N, int64_t K,
                 float scale_a, float scale_b, void* workspace, const GemmPlan& plan,
                 hipStream_t stream) {
-    (void)workspace;
     const float alpha = dtype == MB_DT_FLOAT8_E4M3FN ? scale_a * scale_b : 1.0f;
     switch (plan.variant) {
         case kVariantGeneric:
             return gemm_generic_launch(dtype, A, B, C, M, N, K, alpha, stream);
         case kVariantTiled:
-            return gemm_tiled_launch(dtype, A, B, C, M, N, K, alpha, plan, stream);
+            return gemm_tiled_launch(dtype, A, B, C, M, N, K, alpha, workspace, plan, stream);
         default:
             set_error("GEMM plan variant %d not available", plan.variant);
             return MB_ERR_UNSUPPORTED;

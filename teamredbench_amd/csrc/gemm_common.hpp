@@ -8,8 +8,7 @@ namespace mb {
 
 enum GemmVariant {
     kVariantGeneric = 0,  // any shape, bounds-checked (gemm_generic.hip)
-    kVariantTiled = 1,    // 16-byte aligned rows, LDS-pipelined (gemm_tiled.hip)
-    kVariantSkinny = 2,   // small M, split-K over a workspace (gemm_skinny.hip)
+    kVariantTiled = 1,    // N % 256, LDS-DMA pipelined, optional split-K (gemm_tiled.hip)
 };
 
 // One 16 x 16 MFMA step; operand fragments come from LDS (or registers)
@@ -61,7 +60,7 @@ int gemm_generic_plan(int dtype, int64_t M, int64_t N, int64_t K, GemmPlan* plan
 int gemm_tiled_plan(int dtype, int64_t M, int64_t N, int64_t K, const DeviceProps& props,
                     GemmPlan* plan);
 int gemm_tiled_launch(int dtype, const void* A, const void* B, void* C, int64_t M, int64_t N,
-                      int64_t K, float alpha, const GemmPlan& plan, hipStream_t stream);
+                      int64_t K, float alpha, void* workspace, const GemmPlan& plan, hipStream_t stream);
 int gemm_generic_launch(int dtype, const void* A, const void* B, void* C, int64_t M, int64_t N,
                         int64_t K, float alpha, hipStream_t stream);
 

@@ -207,7 +207,7 @@ template <int DT, int BM, int BN, int WGM, int WGN, int STAGES>
 __global__ void __launch_bounds__(64 * WGM * WGN)
 gemm_tiled_kernel(const unsigned char* __restrict__ A, const unsigned char* __restrict__ B,
                   unsigned char* __restrict__ C, int M, int N, int K, float alpha, int tiles_m,
-                  int tiles_n, int group_m) {
+                  int tiles_n, int group_m, int splits, int k_len, float* __restrict__ ws) {
     typedef Traits<DT> Tr;
     typedef typename Tr::Frag Frag;
     constexpr int W = WGM * WGN;
@@ -247,13 +247,21 @@ gemm_tiled_kernel(const unsigned char* __restrict__ A, const unsigned char* __re
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave / WGN, wn = wave % WGN;
+    // Block -> (tile, K split). With one split the tile index is the block
+    // index (XCD-grouped); with several, the splits of a tile are adjacent.
+    const int split = splits > 1 ? (int)blockIdx.x % splits : 0;
+    const int tile = splits > 1 ? (int)blockIdx.x / splits : (int)blockIdx.x;
     int tm, tn;
-    tile_coords(blockIdx.x, gridDim.x, tiles_m, tiles_n, group_m, &tm, &tn);
+    tile_coords(tile, tiles_m * tiles_n, tiles_m, tiles_n, group_m, &tm, &tn);
     const int lda = K * E;   // bytes per A row
     const int ldb = N * E;   // bytes per B row
+    const int k0 = split * k_len;  // first K element of this block
 
+    // Buffer resources over this block's A row panel and B column panel. The A
+    // range stops at row M, so the rows of a last, partial tile read as zeros.
+    const int a_rows = min(BM, M - tm * BM);
     const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<unsigned char*>(A) + (int64_t)tm * BM * lda, (short)0, BM * lda, kBufferFlags);
+        const_cast<unsigned char*>(A) + (int64_t)tm * BM * lda, (short)0, a_rows * lda, kBufferFlags);
     const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<unsigned char*>(B) + (int64_t)tn * BN * E, (short)0, K * ldb, kBufferFlags);
 
@@ -276,10 +284,10 @@ gemm_tiled_kernel(const unsigned char* __restrict__ A, const unsigned char* __re
 
     auto issue_stage = [&](int kt, unsigned char* slot) {
         const unsigned base = (unsigned)(uintptr_t)(MB_LDS unsigned char*)slot;
-        const int a_soff = kt * kStageK;
+        const int a_soff = k0 * E + kt * kStageK;
 #pragma unroll
         for (int q = 0; q < A_INSTR; ++q) lds_dma16(ra, base + (wave * A_INSTR + q) * 1024, a_voff[q], a_soff);
-        const int b_soff = kt * K_ROWS * ldb;
+        const int b_soff = (k0 + kt * K_ROWS) * ldb;
 #pragma unroll
         for (int q = 0; q < B_INSTR; ++q)
             lds_dma16(rb, base + A_BYTES + (wave * B_INSTR + q) * 1024, b_voff[q], b_soff);
@@ -348,7 +356,7 @@ gemm_tiled_kernel(const unsigned char* __restrict__ A, const unsigned char* __re
     // consumed), so every step issues the same number of loads and the vmcnt
     // bookkeeping stays uniform. The loop is unrolled by STAGES so every slot
     // is a compile-time choice.
-    const int ksteps = K / K_ROWS;
+    const int ksteps = k_len / K_ROWS;
     const int last = ksteps - 1;
     [&]<int... P>(std::integer_sequence<int, P...>) {
         (issue_stage(min(P, last), slot_ptr(std::integral_constant<int, P>{})), ...);
@@ -382,23 +390,59 @@ gemm_tiled_kernel(const unsigned char* __restrict__ A, const unsigned char* __re
     wait_vmcnt_and_barrier<0>();
 
     // Epilogue. Accumulator register r = 4g + q of lane l holds
-    // C[row = 32*i + l % 32][col = 32*j + 8g + 4*(l / 32) + q].
-    const int64_t ldc = (int64_t)N * 2;  // bytes per C row (16-bit output)
-    unsigned char* crow = C + ((int64_t)tm * BM + wm * WTM + (lane & 31)) * ldc;
-    const int64_t ccol = (int64_t)tn * BN + wn * WTN + 4 * half;
+    // C[row = 32*i + l % 32][col = 32*j + 8g + 4*(l / 32) + q]. Rows at or past
+    // M (a partial last tile) are not stored. With K splits the block writes
+    // its unscaled fp32 partial to ws[split][row][col]; a second kernel sums
+    // the splits.
+    const int row0 = tm * BM + wm * WTM + (lane & 31);
+    const int64_t col0 = (int64_t)tn * BN + wn * WTN + 4 * half;
+    if (ws == nullptr) {
+        const int64_t ldc = (int64_t)N * 2;  // bytes per C row (16-bit output)
 #pragma unroll
-    for (int i = 0; i < FM; ++i) {
+        for (int i = 0; i < FM; ++i) {
+            if (row0 + 32 * i >= M) continue;
+            unsigned char* crow = C + (int64_t)(row0 + 32 * i) * ldc;
 #pragma unroll
-        for (int j = 0; j < FN; ++j) {
+            for (int j = 0; j < FN; ++j) {
 #pragma unroll
-            for (int g = 0; g < 4; ++g) {
-                const f32x16& v = acc[i][j];
-                const u32x2 packed = pack4<DT>(v[4 * g] * alpha, v[4 * g + 1] * alpha, v[4 * g + 2] * alpha,
-                                               v[4 * g + 3] * alpha);
-                *reinterpret_cast<u32x2*>(crow + 32 * i * ldc + (ccol + 32 * j + 8 * g) * 2) = packed;
+                for (int g = 0; g < 4; ++g) {
+                    const f32x16& v = acc[i][j];
+                    const u32x2 packed = pack4<DT>(v[4 * g] * alpha, v[4 * g + 1] * alpha, v[4 * g + 2] * alpha,
+                                                   v[4 * g + 3] * alpha);
+                    *reinterpret_cast<u32x2*>(crow + (col0 + 32 * j + 8 * g) * 2) = packed;
+                }
+            }
+        }
+    } else {
+        float* part = ws + (int64_t)split * M * N;
+#pragma unroll
+        for (int i = 0; i < FM; ++i) {
+            if (row0 + 32 * i >= M) continue;
+            float* prow = part + (int64_t)(row0 + 32 * i) * N;
+#pragma unroll
+            for (int j = 0; j < FN; ++j) {
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    const f32x16& v = acc[i][j];
+                    const f32x4 q = {v[4 * g], v[4 * g + 1], v[4 * g + 2], v[4 * g + 3]};
+                    *reinterpret_cast<f32x4*>(prow + col0 + 32 * j + 8 * g) = q;
+                }
             }
         }
     }
+}
+
+// Sum of the K-split partials: C[m][n] = alpha * sum_s ws[s][m][n], rounded
+// once to the output type. Each thread handles 4 consecutive columns.
+template <int DT>
+__global__ void __launch_bounds__(256)
+gemm_splitk_reduce_kernel(const float* __restrict__ ws, unsigned char* __restrict__ C, int64_t quads,
+                          int64_t plane, int splits, float alpha) {
+    const int64_t q = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (q >= quads) return;
+    f32x4 sum = *reinterpret_cast<const f32x4*>(ws + 4 * q);
+    for (int s = 1; s < splits; ++s) sum += *reinterpret_cast<const f32x4*>(ws + s * plane + 4 * q);
+    *reinterpret_cast<u32x2*>(C + 8 * q) = pack4<DT>(sum[0] * alpha, sum[1] * alpha, sum[2] * alpha, sum[3] * alpha);
 }
 
 struct TiledConfig {
@@ -413,22 +457,32 @@ constexpr int kNumConfigs = sizeof(kConfigs) / sizeof(kConfigs[0]);
 
 template <int DT, int CFG>
 int launch_cfg(const void* A, const void* B, void* C, int64_t M, int64_t N, int64_t K, float alpha,
-               hipStream_t stream) {
+               const GemmPlan& plan, void* workspace, hipStream_t stream) {
     constexpr TiledConfig c = kConfigs[CFG];
-    const int tiles_m = (int)(M / c.bm), tiles_n = (int)(N / c.bn);
-    hipLaunchKernelGGL((gemm_tiled_kernel<DT, c.bm, c.bn, c.wgm, c.wgn, c.stages>), dim3(tiles_m * tiles_n),
-                       dim3(64 * c.wgm * c.wgn), 0, stream, static_cast<const unsigned char*>(A),
-                       static_cast<const unsigned char*>(B), static_cast<unsigned char*>(C), (int)M,
-                       (int)N, (int)K, alpha, tiles_m, tiles_n, c.group_m);
+    const int tiles_m = (int)((M + c.bm - 1) / c.bm), tiles_n = (int)(N / c.bn);
+    const int splits = plan.split_k;
+    float* ws = splits > 1 ? static_cast<float*>(workspace) : nullptr;
+    hipLaunchKernelGGL((gemm_tiled_kernel<DT, c.bm, c.bn, c.wgm, c.wgn, c.stages>),
+                       dim3(tiles_m * tiles_n * splits), dim3(64 * c.wgm * c.wgn), 0, stream,
+                       static_cast<const unsigned char*>(A), static_cast<const unsigned char*>(B),
+                       static_cast<unsigned char*>(C), (int)M, (int)N, (int)K, alpha, tiles_m, tiles_n,
+                       c.group_m, splits, (int)(K / splits), ws);
     MB_HIP_TRY(hipGetLastError());
+    if (splits > 1) {
+        const int64_t quads = M * N / 4;
+        hipLaunchKernelGGL(gemm_splitk_reduce_kernel<DT>, dim3((unsigned)((quads + 255) / 256)), dim3(256), 0,
+                           stream, static_cast<const float*>(ws), static_cast<unsigned char*>(C), quads, M * N,
+                           splits, alpha);
+        MB_HIP_TRY(hipGetLastError());
+    }
     return MB_OK;
 }
 
 template <int DT>
-int launch_dtype(int cfg, const void* A, const void* B, void* C, int64_t M, int64_t N, int64_t K,
-                 float alpha, hipStream_t stream) {
-    if (cfg == 0) return launch_cfg<DT, 0>(A, B, C, M, N, K, alpha, stream);
-    return launch_cfg<DT, 1>(A, B, C, M, N, K, alpha, stream);
+int launch_dtype(const GemmPlan& plan, const void* A, const void* B, void* C, int64_t M, int64_t N, int64_t K,
+                 float alpha, void* workspace, hipStream_t stream) {
+    if (plan.config == 0) return launch_cfg<DT, 0>(A, B, C, M, N, K, alpha, plan, workspace, stream);
+    return launch_cfg<DT, 1>(A, B, C, M, N, K, alpha, plan, workspace, stream);
 }
 
 }  // namespace
@@ -440,31 +494,37 @@ int gemm_tiled_plan(int dtype, int64_t M, int64_t N, int64_t K, const DeviceProp
                     GemmPlan* plan) {
     const int64_t e = dtype == MB_DT_FLOAT8_E4M3FN ? 1 : 2;
     const int64_t stage_k = kStageK / e;
-    if (K % stage_k != 0) return MB_ERR_SHAPE;
-    if (K * N * e >= (int64_t(1) << 31) || 256 * K * e >= (int64_t(1) << 31) || M >= (int64_t(1) << 31))
+    if (K % stage_k != 0 || N % 256 != 0) return MB_ERR_SHAPE;
+    if (K * N * e >= (int64_t(1) << 31) || 256 * K * e >= (int64_t(1) << 31) || M >= (int64_t(1) << 31) ||
+        M * N >= (int64_t(1) << 31))
         return MB_ERR_SHAPE;
     const int64_t cus = props.cu_count > 0 ? props.cu_count : 256;
-    auto fits = [&](int i) { return M % kConfigs[i].bm == 0 && N % kConfigs[i].bn == 0; };
-    auto tiles = [&](int i) { return (M / kConfigs[i].bm) * (N / kConfigs[i].bn); };
+    auto tiles = [&](int i) { return ((M + kConfigs[i].bm - 1) / kConfigs[i].bm) * (N / kConfigs[i].bn); };
     int cfg = -1;
     const char* force = std::getenv("MB_GEMM_TILED_CONFIG");  // tuning/testing override
     if (force != nullptr && *force != '\0') {
         const int f = std::atoi(force);
-        if (f >= 0 && f < kNumConfigs && fits(f)) cfg = f;
+        if (f >= 0 && f < kNumConfigs) cfg = f;
     }
-    if (cfg >= 0)
-        ;
-    else if (fits(0) && tiles(0) >= cus)
-        cfg = 0;
-    else if (fits(1))
-        cfg = 1;
-    else if (fits(0))
-        cfg = 0;
-    if (cfg < 0 || tiles(cfg) > INT32_MAX) return MB_ERR_SHAPE;
+    if (cfg < 0) cfg = (tiles(0) >= cus && M % kConfigs[0].bm == 0) ? 0 : 1;
+    // K splits for problems with too few tiles to fill the GPU, as long as the
+    // fp32 partials (splits * M * N * 4 bytes) stay small next to B's bytes.
+    int splits = 1;
+    if (cfg == 1) {
+        while (tiles(cfg) * splits * 2 <= 2 * cus && K % (stage_k * splits * 2) == 0 &&
+               2 * splits * M * 4 <= K * e / 4)
+            splits *= 2;
+    }
+    const char* force_splits = std::getenv("MB_GEMM_SPLITS");  // tuning/testing override
+    if (force_splits != nullptr && *force_splits != '\0') {
+        const int f = std::atoi(force_splits);
+        if (f >= 1 && K % (stage_k * f) == 0) splits = f;
+    }
+    if (tiles(cfg) * splits > INT32_MAX) return MB_ERR_SHAPE;
     const TiledConfig& c = kConfigs[cfg];
     plan->implementation = "gfx950_mfma32_lds_dma";
     plan->threads = 64 * c.wgm * c.wgn;
-    plan->grid = (int)tiles(cfg);
+    plan->grid = (int)(tiles(cfg) * splits);
     plan->tile_m = c.bm;
     plan->tile_n = c.bn;
     plan->tile_k = (int)stage_k;
@@ -476,23 +536,23 @@ int gemm_tiled_plan(int dtype, int64_t M, int64_t N, int64_t K, const DeviceProp
     plan->frag_n = 32;
     plan->frag_k = dtype == MB_DT_FLOAT8_E4M3FN ? 64 : 16;
     plan->k_stages = c.stages;
-    plan->split_k = 1;
+    plan->split_k = splits;
     plan->tile_group_m = c.group_m;
-    plan->workspace = 0;
+    plan->workspace = splits > 1 ? (size_t)splits * (size_t)M * (size_t)N * sizeof(float) : 0;
     plan->variant = kVariantTiled;
     plan->config = cfg;
     return MB_OK;
 }
 
 int gemm_tiled_launch(int dtype, const void* A, const void* B, void* C, int64_t M, int64_t N,
-                      int64_t K, float alpha, const GemmPlan& plan, hipStream_t stream) {
+                      int64_t K, float alpha, void* workspace, const GemmPlan& plan, hipStream_t stream) {
     switch (dtype) {
         case MB_DT_BFLOAT16:
-            return launch_dtype<MB_DT_BFLOAT16>(plan.config, A, B, C, M, N, K, alpha, stream);
+            return launch_dtype<MB_DT_BFLOAT16>(plan, A, B, C, M, N, K, alpha, workspace, stream);
         case MB_DT_FLOAT16:
-            return launch_dtype<MB_DT_FLOAT16>(plan.config, A, B, C, M, N, K, alpha, stream);
+            return launch_dtype<MB_DT_FLOAT16>(plan, A, B, C, M, N, K, alpha, workspace, stream);
         case MB_DT_FLOAT8_E4M3FN:
-            return launch_dtype<MB_DT_FLOAT8_E4M3FN>(plan.config, A, B, C, M, N, K, alpha, stream);
+            return launch_dtype<MB_DT_FLOAT8_E4M3FN>(plan, A, B, C, M, N, K, alpha, workspace, stream);
         default:
             set_error("tiled GEMM: unsupported dtype %d", dtype);
             return MB_ERR_UNSUPPORTED;

@@ -75,6 +75,46 @@ def test_tiled_configurations(lib, dtype, config, shape, monkeypatch):
 
 
 @pytest.mark.parametrize("dtype", ["bfloat16", "float16", "float8_e4m3fn"])
+@pytest.mark.parametrize("shape", [(1, 4096, 4096), (16, 8192, 8192), (128, 8192, 8192), (100, 2048, 4096)])
+def test_skinny_shapes_split_k(lib, dtype, shape):
+    # The skinny GEMM configurations: ragged M on the tiled kernel, K split
+    # over an fp32 workspace and summed by the reduction kernel.
+    m, n, k = shape
+    info = lib.gemm_info(capi.DTYPES[dtype], m, n, k)
+    splits = info["split_k"]
+    assert info["implementation"] == "gfx950_mfma32_lds_dma" and splits >= 2
+    assert info["workspace_bytes"] == splits * m * n * 4
+    print(f"[gemm] skinny {dtype} {shape} split {splits}", flush=True)
+    _check_random(lib, dtype, m, n, k, seed=m)
+
+
+@pytest.mark.parametrize("dtype", ["bfloat16", "float8_e4m3fn"])
+@pytest.mark.parametrize("m", [1, 31, 127, 129, 300])
+@pytest.mark.parametrize("splits", ["1", "2", "3"])
+def test_ragged_m_and_forced_splits(lib, dtype, m, splits, monkeypatch):
+    monkeypatch.setenv("MB_GEMM_SPLITS", splits)
+    n, k = 512, 384
+    info = lib.gemm_info(capi.DTYPES[dtype], m, n, k)
+    assert info["split_k"] == int(splits)
+    print(f"[gemm] ragged m={m} {dtype} splits={splits}", flush=True)
+    _check_random(lib, dtype, m, n, k, seed=m + 7)
+
+
+def test_workspace_too_small_is_rejected(lib):
+    m, n, k = 16, 8192, 8192
+    need = lib.gemm_workspace_size(capi.DT_BFLOAT16, m, n, k)
+    assert need > 0
+    a = torch.zeros(m, k, dtype=torch.bfloat16, device="cuda")
+    b = torch.zeros(k, n, dtype=torch.bfloat16, device="cuda")
+    c = torch.zeros(m, n, dtype=torch.bfloat16, device="cuda")
+    ws = torch.empty(need // 2, dtype=torch.uint8, device="cuda")
+    with pytest.raises(capi.NativeLibraryError) as err:
+        lib.gemm(capi.DT_BFLOAT16, a.data_ptr(), b.data_ptr(), c.data_ptr(), m, n, k, 1.0, 1.0, ws.data_ptr(),
+                 need // 2)
+    assert err.value.status == capi.MB_ERR_WORKSPACE
+
+
+@pytest.mark.parametrize("dtype", ["bfloat16", "float16", "float8_e4m3fn"])
 def test_large_square_takes_the_big_tile(lib, dtype):
     m = n = k = 4096
     info = lib.gemm_info(capi.DTYPES[dtype], m, n, k)
