@@ -125,55 +125,35 @@ struct Traits<MB_DT_FLOAT8_E4M3FN> {
     }
 };
 
-// A operand of substep s for this lane: row `row` of the stage, K elements
-// 8*(lane/32) .. +7 of the substep (16-bit) or 32*(lane/32) .. +31 (fp8).
-template <int DT>
-__device__ __forceinline__ typename Traits<DT>::Frag read_a(const unsigned char* st, int row, int s, int half) {
-    const unsigned char* p = st + row * kStageK;
-    const int f = swz_a(row);
-    if constexpr (Traits<DT>::kElem == 2) {
-        return *reinterpret_cast<const u32x4*>(p + (((2 * s + half) ^ f) << 4));
-    } else {
-        const u32x4 lo = *reinterpret_cast<const u32x4*>(p + (((2 * half) ^ f) << 4));
-        const u32x4 hi = *reinterpret_cast<const u32x4*>(p + (((2 * half + 1) ^ f) << 4));
-        return __builtin_bit_cast(i32x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
-    }
+// One 16-byte piece of this lane's A operand: row `row` of the stage, 16-byte
+// K chunk `chunk` (16-bit: chunk 2s + lane/32 of substep s; fp8: chunks
+// 2*(lane/32) and +1 form the 32-byte operand).
+__device__ __forceinline__ u32x4 read_a_piece(const unsigned char* st, int row, int chunk) {
+    return *reinterpret_cast<const u32x4*>(st + row * kStageK + ((chunk ^ swz_a(row)) << 4));
 }
 
-// B operand of substep s for this lane: column nb + lane % 32, the same K
-// range as read_a. `st` is the B part of the stage (rows of BN * elem bytes).
+// One transposing read of this lane's B operand (column nb + lane % 32).
+// 16-bit: 4 K-rows x 16 columns per 16-lane group, part t (0..1) of substep s
+// gives K 16s + 8*(lane/32) + 4t .. +3. fp8: 8 K-rows x 16 columns, part t
+// (0..3) gives K 32*(lane/32) + 8t .. +7. `st` is the B part of the stage.
 template <int DT, int BN>
-__device__ __forceinline__ typename Traits<DT>::Frag read_b(const unsigned char* st, int nb, int s, int lane) {
+__device__ __forceinline__ u32x2 read_b_piece(const unsigned char* st, int nb, int s, int t, int lane) {
     const int g = lane >> 4, i = lane & 15;
     if constexpr (Traits<DT>::kElem == 2) {
-        // Two transposing reads of 4 K-rows x 16 columns per 16-lane group.
         constexpr int row_bytes = BN * 2;
-        u32x2 part[2];
-#pragma unroll
-        for (int t = 0; t < 2; ++t) {
-            const int k = 16 * s + 8 * (g >> 1) + 4 * t + (i >> 2);
-            const int n = nb + 16 * (g & 1) + 4 * (i & 3);
-            const int off = k * row_bytes + (((n >> 3) ^ swz_b16(k & 3)) << 4) + 8 * (i & 1);
-            const bf16x4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
-                (MB_LDS bf16x4_t*)((MB_LDS unsigned char*)st + off));
-            part[t] = __builtin_bit_cast(u32x2, v);
-        }
-        return __builtin_shufflevector(part[0], part[1], 0, 1, 2, 3);
+        const int k = 16 * s + 8 * (g >> 1) + 4 * t + (i >> 2);
+        const int n = nb + 16 * (g & 1) + 4 * (i & 3);
+        const int off = k * row_bytes + (((n >> 3) ^ swz_b16(k & 3)) << 4) + 8 * (i & 1);
+        const bf16x4_t v =
+            __builtin_amdgcn_ds_read_tr16_b64_v4bf16((MB_LDS bf16x4_t*)((MB_LDS unsigned char*)st + off));
+        return __builtin_bit_cast(u32x2, v);
     } else {
-        // Four transposing reads of 8 K-rows x 16 columns per 16-lane group.
         constexpr int row_bytes = BN;
-        u32x2 part[4];
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            const int k = 32 * (g >> 1) + 8 * t + (i >> 1);
-            const int n = nb + 16 * (g & 1) + 8 * (i & 1);
-            const int off = k * row_bytes + (((n >> 4) ^ swz_b8(k & 7)) << 4) + 8 * (i & 1);
-            const i32x2_t v = __builtin_amdgcn_ds_read_tr8_b64_v2i32((MB_LDS i32x2_t*)((MB_LDS unsigned char*)st + off));
-            part[t] = __builtin_bit_cast(u32x2, v);
-        }
-        const u32x4 lo = __builtin_shufflevector(part[0], part[1], 0, 1, 2, 3);
-        const u32x4 hi = __builtin_shufflevector(part[2], part[3], 0, 1, 2, 3);
-        return __builtin_bit_cast(i32x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+        const int k = 32 * (g >> 1) + 8 * t + (i >> 1);
+        const int n = nb + 16 * (g & 1) + 8 * (i & 1);
+        const int off = k * row_bytes + (((n >> 4) ^ swz_b8(k & 7)) << 4) + 8 * (i & 1);
+        const i32x2_t v = __builtin_amdgcn_ds_read_tr8_b64_v2i32((MB_LDS i32x2_t*)((MB_LDS unsigned char*)st + off));
+        return __builtin_bit_cast(u32x2, v);
     }
 }
 
@@ -282,6 +262,17 @@ gemm_tiled_kernel(const unsigned char* __restrict__ A, const unsigned char* __re
         b_voff[q] = row * ldb + ((pchunk ^ f) << 4);
     }
 
+    // DMA instruction q (A pieces first, then B) of stage kt into `slot`.
+    auto issue_one = [&](int kt, unsigned char* slot, auto idx) {
+        constexpr int q = decltype(idx)::value;
+        const unsigned base = (unsigned)(uintptr_t)(MB_LDS unsigned char*)slot;
+        if constexpr (q < A_INSTR) {
+            lds_dma16(ra, base + (wave * A_INSTR + q) * 1024, a_voff[q], k0 * E + kt * kStageK);
+        } else {
+            constexpr int qb = q - A_INSTR;
+            lds_dma16(rb, base + A_BYTES + (wave * B_INSTR + qb) * 1024, b_voff[qb], (k0 + kt * K_ROWS) * ldb);
+        }
+    };
     auto issue_stage = [&](int kt, unsigned char* slot) {
         const unsigned base = (unsigned)(uintptr_t)(MB_LDS unsigned char*)slot;
         const int a_soff = k0 * E + kt * kStageK;
@@ -313,43 +304,74 @@ gemm_tiled_kernel(const unsigned char* __restrict__ A, const unsigned char* __re
         Frag a[FM];
         Frag b[FN];
     };
-    constexpr int FM_HALF = Tr::kSub == 2 ? FM : FM / 2;
-    static_assert(Tr::kSub == 2 || FM % 2 == 0, "fp8 halves split the A fragments");
-    auto read_half = [&](const unsigned char* slot, auto part, Ops& o) {
-        constexpr int p = decltype(part)::value;
-        const unsigned char* sa = slot;
+    constexpr bool kWide = Tr::kElem == 1;            // fp8: 32-byte operands
+    constexpr int FM_HALF = kWide ? FM / 2 : FM;
+    constexpr int B_PIECES = kWide ? 4 : 2;           // transposing reads per B fragment
+    constexpr int A_PIECES = kWide ? 2 : 1;           // 16-byte reads per A fragment
+    static_assert(!kWide || FM % 2 == 0, "fp8 halves split the A fragments");
+    // LDS reads that fill the operands of half P, and the MFMAs of a half.
+    constexpr int kReads0 = (kWide ? FN * B_PIECES : FN * B_PIECES) + FM_HALF * A_PIECES;
+    constexpr int kReads1 = (kWide ? 0 : FN * B_PIECES) + FM_HALF * A_PIECES;
+    constexpr int kMfmas = FM_HALF * FN;
+
+    // Read number r of half P of the stage in `slot` into o (B pieces first).
+    auto read_one = [&](const unsigned char* slot, auto part, auto idx, Ops& o) {
+        constexpr int P = decltype(part)::value;
+        constexpr int r = decltype(idx)::value;
+        constexpr int nb_reads = (kWide && P == 1) ? 0 : FN * B_PIECES;
         const unsigned char* sb = slot + A_BYTES;
-        if constexpr (Tr::kSub == 2) {
-#pragma unroll
-            for (int j = 0; j < FN; ++j) o.b[j] = read_b<DT, BN>(sb, b_col + 32 * j, p, lane);
-#pragma unroll
-            for (int i = 0; i < FM; ++i) o.a[i] = read_a<DT>(sa, a_row + 32 * i, p, half);
+        if constexpr (r < nb_reads) {
+            constexpr int j = r / B_PIECES, t = r % B_PIECES;
+            const u32x2 v = read_b_piece<DT, BN>(sb, b_col + 32 * j, kWide ? 0 : P, t, lane);
+            o.b[j][2 * t] = v[0];
+            o.b[j][2 * t + 1] = v[1];
         } else {
-            if constexpr (p == 0) {
+            constexpr int q = r - nb_reads;
+            constexpr int i = (kWide ? P * FM_HALF : 0) + q / A_PIECES, e = q % A_PIECES;
+            const int chunk = kWide ? 2 * half + e : 2 * P + half;
+            const u32x4 v = read_a_piece(slot, a_row + 32 * i, chunk);
 #pragma unroll
-                for (int j = 0; j < FN; ++j) o.b[j] = read_b<DT, BN>(sb, b_col + 32 * j, 0, lane);
-            }
-#pragma unroll
-            for (int i = p * FM_HALF; i < (p + 1) * FM_HALF; ++i) o.a[i] = read_a<DT>(sa, a_row + 32 * i, 0, half);
+            for (int w = 0; w < 4; ++w) o.a[i][4 * e + w] = v[w];
         }
     };
-    auto mfma_half = [&](auto part, const Ops& o) {
-        constexpr int p = decltype(part)::value;
-        constexpr int i0 = Tr::kSub == 2 ? 0 : p * FM_HALF;
-#pragma unroll
-        for (int i = i0; i < i0 + FM_HALF; ++i)
-#pragma unroll
-            for (int j = 0; j < FN; ++j) acc[i][j] = Tr::mfma(o.b[j], o.a[i], acc[i][j]);
+    auto mfma_one = [&](auto part, auto idx, const Ops& o) {
+        constexpr int P = decltype(part)::value;
+        constexpr int q = decltype(idx)::value;
+        constexpr int i = (kWide ? P * FM_HALF : 0) + q / FN, j = q % FN;
+        acc[i][j] = Tr::mfma(o.b[j], o.a[i], acc[i][j]);
     };
     using Half0 = std::integral_constant<int, 0>;
     using Half1 = std::integral_constant<int, 1>;
 
+    // Runs the MFMAs of one half with `nmem` memory operations spread between
+    // them (front-loaded, at most two after each MFMA); sched_barrier(0) pins
+    // the order so the MFMA pipe never waits on a burst of issues.
+    auto interleave = [&](auto part, const Ops& o, auto nmem, auto&& mem) {
+        constexpr int N_MEM = decltype(nmem)::value;
+        [&]<int... Q>(std::integer_sequence<int, Q...>) {
+            ([&] {
+                mfma_one(part, std::integral_constant<int, Q>{}, o);
+                constexpr int lo = Q * 2, hi = Q * 2 + 2 < N_MEM ? Q * 2 + 2 : N_MEM;
+                if constexpr (Q == kMfmas - 1) {
+                    [&]<int... R>(std::integer_sequence<int, R...>) {
+                        (mem(std::integral_constant<int, lo + R>{}), ...);
+                    }(std::make_integer_sequence<int, (N_MEM > lo ? N_MEM - lo : 0)>{});
+                } else if constexpr (hi > lo) {
+                    [&]<int... R>(std::integer_sequence<int, R...>) {
+                        (mem(std::integral_constant<int, lo + R>{}), ...);
+                    }(std::make_integer_sequence<int, hi - lo>{});
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            }(), ...);
+        }(std::make_integer_sequence<int, kMfmas>{});
+    };
+
     // Software pipeline over a ring of STAGES slots, one barrier per stage:
     //   step kt (stage kt in slot kt % STAGES, its half-0 operands in `next`):
-    //     read half 1 of stage kt          | MFMAs of half 0 run meanwhile
+    //     MFMAs of half 0, with the LDS reads of half 1 of stage kt between them
     //     wait for this wave's loads of stage kt+1, barrier
-    //     load stage kt+STAGES-1 into the slot stage kt-1 used
-    //     read half 0 of stage kt+1        | MFMAs of half 1 run meanwhile
+    //     MFMAs of half 1, with the loads of stage kt+STAGES-1 (into the slot
+    //     stage kt-1 used) and the LDS reads of half 0 of stage kt+1 between them
     // The barrier certifies stage kt+1 for every wave and that every wave is
     // done reading slot kt-1 (those reads fed MFMAs before the barrier).
     // Loads past the last stage re-read the last stage (in bounds, never
@@ -363,24 +385,29 @@ gemm_tiled_kernel(const unsigned char* __restrict__ A, const unsigned char* __re
     }(std::make_integer_sequence<int, STAGES - 1>{});
     Ops next;
     wait_vmcnt_and_barrier<LOADS * (STAGES - 2)>();
-    read_half(slot_ptr(std::integral_constant<int, 0>{}), Half0{}, next);
+    [&]<int... R>(std::integer_sequence<int, R...>) {
+        (read_one(slot_ptr(std::integral_constant<int, 0>{}), Half0{}, std::integral_constant<int, R>{}, next), ...);
+    }(std::make_integer_sequence<int, kReads0>{});
 
     auto step = [&](auto idx, int kt) {
         constexpr int I = decltype(idx)::value;
-        // sched_barrier(0) keeps the scheduler from hoisting MFMAs above the
-        // LDS reads meant to overlap them.
+        const unsigned char* cur_slot = slot_ptr(idx);
+        const unsigned char* next_slot = slot_ptr(std::integral_constant<int, (I + 1) % STAGES>{});
+        unsigned char* load_slot = slot_ptr(std::integral_constant<int, (I + STAGES - 1) % STAGES>{});
         const Ops cur0 = next;
         Ops cur1 = cur0;  // fp8 keeps the B fragments of half 0
-        read_half(slot_ptr(idx), Half1{}, cur1);
-        __builtin_amdgcn_sched_barrier(0);
-        mfma_half(Half0{}, cur0);
-        __builtin_amdgcn_sched_barrier(0);
+        interleave(Half0{}, cur0, std::integral_constant<int, kReads1>{},
+                   [&](auto r) { read_one(cur_slot, Half1{}, r, cur1); });
         wait_vmcnt_and_barrier<LOADS * (STAGES - 3)>();
-        issue_stage(min(kt + STAGES - 1, last), slot_ptr(std::integral_constant<int, (I + STAGES - 1) % STAGES>{}));
-        read_half(slot_ptr(std::integral_constant<int, (I + 1) % STAGES>{}), Half0{}, next);
-        __builtin_amdgcn_sched_barrier(0);
-        mfma_half(Half1{}, cur1);
-        __builtin_amdgcn_sched_barrier(0);
+        const int kload = min(kt + STAGES - 1, last);
+        interleave(Half1{}, cur1, std::integral_constant<int, LOADS + kReads0>{}, [&](auto m) {
+            constexpr int q = decltype(m)::value;
+            if constexpr (q < LOADS) {
+                issue_one(kload, load_slot, std::integral_constant<int, q>{});
+            } else {
+                read_one(next_slot, Half0{}, std::integral_constant<int, q - LOADS>{}, next);
+            }
+        });
     };
     for (int kt = 0; kt < ksteps; kt += STAGES) {
         [&]<int... I>(std::integer_sequence<int, I...>) {
