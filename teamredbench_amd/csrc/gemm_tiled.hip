@@ -343,24 +343,21 @@ gemm_tiled_kernel(const unsigned char* __restrict__ A, const unsigned char* __re
     using Half0 = std::integral_constant<int, 0>;
     using Half1 = std::integral_constant<int, 1>;
 
-    // Runs the MFMAs of one half with `nmem` memory operations spread between
-    // them (front-loaded, at most two after each MFMA); sched_barrier(0) pins
-    // the order so the MFMA pipe never waits on a burst of issues.
+    // Runs the MFMAs of one half with `nmem` memory operations spread evenly
+    // between them (front-loaded: ceil(nmem / MFMAs) after each MFMA);
+    // sched_barrier(0) pins the order so the MFMA pipe never waits on a burst
+    // of issues.
     auto interleave = [&](auto part, const Ops& o, auto nmem, auto&& mem) {
         constexpr int N_MEM = decltype(nmem)::value;
+        constexpr int PER = (N_MEM + kMfmas - 1) / kMfmas;
         [&]<int... Q>(std::integer_sequence<int, Q...>) {
             ([&] {
                 mfma_one(part, std::integral_constant<int, Q>{}, o);
-                constexpr int lo = Q * 2, hi = Q * 2 + 2 < N_MEM ? Q * 2 + 2 : N_MEM;
-                if constexpr (Q == kMfmas - 1) {
-                    [&]<int... R>(std::integer_sequence<int, R...>) {
-                        (mem(std::integral_constant<int, lo + R>{}), ...);
-                    }(std::make_integer_sequence<int, (N_MEM > lo ? N_MEM - lo : 0)>{});
-                } else if constexpr (hi > lo) {
-                    [&]<int... R>(std::integer_sequence<int, R...>) {
-                        (mem(std::integral_constant<int, lo + R>{}), ...);
-                    }(std::make_integer_sequence<int, hi - lo>{});
-                }
+                constexpr int lo = Q * PER < N_MEM ? Q * PER : N_MEM;
+                constexpr int hi = Q * PER + PER < N_MEM ? Q * PER + PER : N_MEM;
+                [&]<int... R>(std::integer_sequence<int, R...>) {
+                    (mem(std::integral_constant<int, lo + R>{}), ...);
+                }(std::make_integer_sequence<int, hi - lo>{});
                 __builtin_amdgcn_sched_barrier(0);
             }(), ...);
         }(std::make_integer_sequence<int, kMfmas>{});
@@ -370,8 +367,8 @@ gemm_tiled_kernel(const unsigned char* __restrict__ A, const unsigned char* __re
     //   step kt (stage kt in slot kt % STAGES, its half-0 operands in `next`):
     //     MFMAs of half 0, with the LDS reads of half 1 of stage kt between them
     //     wait for this wave's loads of stage kt+1, barrier
-    //     MFMAs of half 1, with the loads of stage kt+STAGES-1 (into the slot
-    //     stage kt-1 used) and the LDS reads of half 0 of stage kt+1 between them
+    //     MFMAs of half 1, with the LDS reads of half 0 of stage kt+1 and the
+    //     loads of stage kt+STAGES-1 (into the slot stage kt-1 used) between them
     // The barrier certifies stage kt+1 for every wave and that every wave is
     // done reading slot kt-1 (those reads fed MFMAs before the barrier).
     // Loads past the last stage re-read the last stage (in bounds, never
@@ -400,12 +397,13 @@ gemm_tiled_kernel(const unsigned char* __restrict__ A, const unsigned char* __re
                    [&](auto r) { read_one(cur_slot, Half1{}, r, cur1); });
         wait_vmcnt_and_barrier<LOADS * (STAGES - 3)>();
         const int kload = min(kt + STAGES - 1, last);
+        // Operand reads first (they feed the next MFMAs), the loads after them.
         interleave(Half1{}, cur1, std::integral_constant<int, LOADS + kReads0>{}, [&](auto m) {
             constexpr int q = decltype(m)::value;
-            if constexpr (q < LOADS) {
-                issue_one(kload, load_slot, std::integral_constant<int, q>{});
+            if constexpr (q < kReads0) {
+                read_one(next_slot, Half0{}, std::integral_constant<int, q>{}, next);
             } else {
-                read_one(next_slot, Half0{}, std::integral_constant<int, q - LOADS>{}, next);
+                issue_one(kload, load_slot, std::integral_constant<int, q - kReads0>{});
             }
         });
     };
