@@ -1,0 +1,95 @@
+"""The gfx950 kernels against the reference's own native executables (-m gpu).
+
+`oracle/Makefile ref` compiles the reference's HIP sources
+(src/teamredbench/native/kernels/hbm_bandwidth.hip.cpp and mfu_gemm.hip.cpp)
+for gfx950 into oracle/_ref/. Each case runs the reference executable with
+its own argv contract (benchmarks/hbm.py:95-113, mfu.py:107-125), reads
+`elapsed_s` from its JSON line, times the same workload through the C ABI
+on inputs of the same kind (the reference zero-fills the stream arrays and
+fills the GEMM operands with 0.03125), and requires the gfx950 kernel to
+match or beat it. The figures are also written to
+gpurun_out/vs_reference_native.json when that directory exists.
+"""
+from __future__ import annotations
+
+import json
+from pathlib import Path
+import subprocess
+
+import pytest
+import torch
+
+from teamredbench_amd.native import capi
+
+pytestmark = pytest.mark.gpu
+
+ROOT = Path(__file__).resolve().parent.parent
+REF = ROOT / "oracle" / "_ref"
+RESULTS: dict[str, dict] = {}
+
+
+def _run_ref(binary: str, args: list[str]) -> float:
+    path = REF / binary
+    if not path.exists():
+        pytest.skip(f"{path} not built (oracle/Makefile ref needs the reference sources)")
+    proc = subprocess.run([str(path), *args], capture_output=True, text=True, timeout=300)
+    assert proc.returncode == 0, proc.stderr
+    line = [ln for ln in proc.stdout.splitlines() if ln.strip()][-1]
+    payload = json.loads(line)
+    assert payload["status"] == "ok", payload
+    return float(payload["raw_metrics"]["elapsed_s"])
+
+
+def _record(key: str, **values) -> None:
+    RESULTS[key] = values
+    out = ROOT / "gpurun_out"
+    if out.is_dir():
+        (out / "vs_reference_native.json").write_text(json.dumps(RESULTS, indent=1), encoding="utf-8")
+    print(f"[vs-reference] {key}: {values}", flush=True)
+
+
+@pytest.mark.parametrize("mode, factor", [("triad", 3), ("copy", 2), ("scale", 2)])
+def test_stream_fp32_1024mib_matches_or_beats_reference(lib, mode, factor):
+    n = 1024 * 1024 * 1024 // 4
+    ref_s = _run_ref("hbm_hip", ["--dtype", "float32", "--mode", mode, "--size-mib", "1024", "--warmup", "10",
+                                 "--iterations", "50", "--device-id", "0", "--scale", "3.0"])
+    b = torch.zeros(n, device="cuda")
+    c = torch.zeros(n, device="cuda")
+    a = torch.empty_like(b)
+    ours_s = lib.time_stream(capi.OPS[mode], capi.DT_FLOAT32, a.data_ptr(), b.data_ptr(), c.data_ptr(), n, 3.0, 0,
+                             10, 50, torch.cuda.current_stream().cuda_stream)
+    moved = factor * 4 * n
+    _record(f"stream_{mode}_fp32_1024MiB", reference_gbps=moved / ref_s / 1e9, ours_gbps=moved / ours_s / 1e9)
+    assert ours_s <= ref_s * 1.02, f"{mode}: ours {moved / ours_s / 1e9:.0f} GB/s vs reference {moved / ref_s / 1e9:.0f}"
+
+
+@pytest.mark.parametrize("dtype", ["bfloat16", "float16"])
+def test_gemm_8192_matches_or_beats_reference(lib, dtype):
+    m = n = k = 8192
+    ref_s = _run_ref("mfu_hipblas", ["--dtype", dtype, "--m", str(m), "--n", str(n), "--k", str(k), "--warmup", "3",
+                                     "--iterations", "10", "--device-id", "0"])
+    tdt = getattr(torch, dtype)
+    a = torch.full((m, k), 0.03125, dtype=tdt, device="cuda")
+    b = torch.full((k, n), 0.03125, dtype=tdt, device="cuda")
+    c = torch.empty((m, n), dtype=tdt, device="cuda")
+    dt = capi.DTYPES[dtype]
+    ws_bytes = lib.gemm_workspace_size(dt, m, n, k)
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device="cuda")
+    ours_s = lib.time_gemm(dt, a.data_ptr(), b.data_ptr(), c.data_ptr(), m, n, k, 1.0, 1.0, ws.data_ptr(), ws_bytes,
+                           3, 10, torch.cuda.current_stream().cuda_stream)
+    assert torch.all(c[::1024, ::1024].float() == k / 1024)  # the constant fill's known answer
+    flops = 2.0 * m * n * k
+    _record(f"gemm_{dtype}_8192", reference_tflops=flops / ref_s / 1e12, ours_tflops=flops / ours_s / 1e12)
+    assert ours_s <= ref_s * 1.02, f"{dtype}: ours {flops / ours_s / 1e12:.0f} TFLOPS vs reference {flops / ref_s / 1e12:.0f}"
+
+
+def test_reference_has_no_fp8_gemm(lib):
+    path = REF / "mfu_hipblas"
+    if not path.exists():
+        pytest.skip("reference executable not built")
+    proc = subprocess.run([str(path), "--dtype", "float8_e4m3fn", "--m", "256", "--n", "256", "--k", "256",
+                           "--warmup", "0", "--iterations", "1", "--device-id", "0"],
+                          capture_output=True, text=True, timeout=120)
+    payload = json.loads([ln for ln in proc.stdout.splitlines() if ln.strip()][-1])
+    assert payload["status"] == "skipped"          # mfu_gemm.hip.cpp:9-21
+    assert lib.gemm_info(capi.DT_FLOAT8_E4M3FN, 256, 256, 256)["implementation"]  # ours takes it
