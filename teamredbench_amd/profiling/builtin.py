@@ -10,29 +10,42 @@ in separate passes). :func:`collect` parses the CSV artifacts into a
 per-kernel summary attached to the metadata sidecar:
 
   stream kernels: dram_fetch_bytes / dram_write_bytes per dispatch and the
-                  counter-derived GB/s = (FETCH_SIZE + WRITE_SIZE) * 1024 / duration
-  GEMM kernels:   mfma_busy_pct = SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE * CUs * 4)
+                  counter-derived GB/s = (fetch + write bytes) / duration, with
+                  FETCH_SIZE and WRITE_SIZE (KiB per dispatch) each scaled by a
+                  calibration factor: every pass that collects one of them is
+                  also run once over a plain copy kernel of known traffic
+                  (teamredbench_amd.profiling.stream_probe --ops copy), and the
+                  factor makes that copy's reading equal its known bytes (on
+                  MI355X FETCH_SIZE reads half the bytes moved)
+  GEMM kernels:   mfma_busy_pct = SQ_VALU_MFMA_BUSY_CYCLES /
+                  (GRBM_GUI_ACTIVE / XCDs * CUs * 4 SIMDs); GRBM_GUI_ACTIVE is
+                  summed over the XCDs
 
 Params (suite ``profiling.params``): binary (default rocprofv3), stats
 (bool, default true), kernel_include_regex, counter_passes (list of counter
 lists; default the three passes above; [] disables counters), hip_trace
-(bool; only on the trace pass), extra_args, env.
+(bool; only on the trace pass), calibrate (bool, default true), extra_args,
+env.
 The engine is registered as ``rocprofv3`` and, for suites written for the
 reference, as ``rocprof``.
 """
 from __future__ import annotations
 
 import csv
+import json
 import os
 from pathlib import Path
 import shutil
 from statistics import mean
+import sys
 from typing import Any
 
 from teamredbench_amd.profiling.registry import ProfilingLaunch, register_profile_engine
 
 DEFAULT_COUNTER_PASSES = [["FETCH_SIZE"], ["WRITE_SIZE"], ["SQ_VALU_MFMA_BUSY_CYCLES", "GRBM_GUI_ACTIVE"]]
 SIMDS_PER_CU = 4
+CALIBRATION_ELEMENTS = 1 << 26          # fp32 copy: reads and writes 256 MiB
+CALIBRATION_KERNEL = "stream_vec_kernel<0, "  # the library's copy kernel
 
 
 def _resolve(base: Path | None, value: str) -> Path:
@@ -78,6 +91,19 @@ def _build_rocprofv3_command(params: dict[str, Any], target_command: list[str], 
                *_common(params), "--"])
         for i, group in enumerate(passes)
     )
+    standalone: list[tuple[str, ...]] = []
+    if params.get("calibrate", True):
+        for i, group in enumerate(passes):
+            if not {"FETCH_SIZE", "WRITE_SIZE"} & set(map(str, group)):
+                continue
+            standalone.append(tuple([
+                binary, "--pmc", *map(str, group), "-d", str(artifact_dir / f"cal{i + 1}"), "-o", "run", "-f", "csv",
+                "--", sys.executable, "-m", "teamredbench_amd.profiling.stream_probe", "--ops", "copy",
+                "--elements", str(CALIBRATION_ELEMENTS), "--launches", "3",
+            ]))
+        (artifact_dir / "calibration.json").write_text(json.dumps({
+            "kernel": CALIBRATION_KERNEL, "read_bytes": 4 * CALIBRATION_ELEMENTS,
+            "write_bytes": 4 * CALIBRATION_ELEMENTS}), encoding="utf-8")
     env: dict[str, str] = {}
     rocm_bin = Path(os.environ.get("ROCM_PATH", "/opt/rocm")) / "bin"
     env["PATH"] = os.pathsep.join([str(rocm_bin), os.environ.get("PATH", "")])
@@ -89,6 +115,7 @@ def _build_rocprofv3_command(params: dict[str, Any], target_command: list[str], 
         env=env,
         metadata={"binary": binary, "counter_passes": passes, "trace_dir": str(artifact_dir / "trace")},
         extra_passes=extra,
+        standalone_passes=tuple(standalone),
         collect=collect,
     )
 
@@ -138,7 +165,26 @@ def parse_counters(pmc_dir: Path) -> dict[str, dict[str, float]]:
     return {k: {c: mean(v) for c, v in counters.items()} for k, counters in grouped.items()}
 
 
-def collect(artifact_dir: Path, cu_count: int | None = None) -> dict[str, Any]:
+def calibration_factors(artifact_dir: Path) -> dict[str, float]:
+    """FETCH_SIZE / WRITE_SIZE scale factors from the calibration passes:
+    known bytes of the copy kernel / (counter KiB * 1024)."""
+    spec_path = artifact_dir / "calibration.json"
+    if not spec_path.exists():
+        return {}
+    spec = json.loads(spec_path.read_text(encoding="utf-8"))
+    factors: dict[str, float] = {}
+    for cal_dir in sorted(artifact_dir.glob("cal*")):
+        for kernel, values in parse_counters(cal_dir).items():
+            if spec["kernel"] not in kernel:
+                continue
+            if values.get("FETCH_SIZE"):
+                factors["FETCH_SIZE"] = spec["read_bytes"] / (values["FETCH_SIZE"] * 1024.0)
+            if values.get("WRITE_SIZE"):
+                factors["WRITE_SIZE"] = spec["write_bytes"] / (values["WRITE_SIZE"] * 1024.0)
+    return factors
+
+
+def collect(artifact_dir: Path, cu_count: int | None = None, xcd_count: int | None = None) -> dict[str, Any]:
     """Per-kernel summary from a rocprofv3 artifact directory (trace + pmc passes)."""
     kernels = parse_kernel_trace(artifact_dir / "trace") if (artifact_dir / "trace").exists() else {}
     counters: dict[str, dict[str, float]] = {}
@@ -146,22 +192,30 @@ def collect(artifact_dir: Path, cu_count: int | None = None) -> dict[str, Any]:
         for kernel, values in parse_counters(pmc_dir).items():
             counters.setdefault(kernel, {}).update(values)
     cus = cu_count or int(os.environ.get("MB_CU_COUNT", "256"))
-    summary: dict[str, Any] = {}
+    xcds = xcd_count or int(os.environ.get("MB_XCD_COUNT", "8"))
+    factors = calibration_factors(artifact_dir)
+    summary: dict[str, Any] = {"_calibration": factors} if factors else {}
     for name in sorted(set(kernels) | set(counters)):
         entry: dict[str, Any] = dict(kernels.get(name, {}))
         values = counters.get(name, {})
         entry["counters"] = values
         duration = entry.get("avg_duration_ns")
+        fetch = write = None
         if "FETCH_SIZE" in values:
-            entry["dram_fetch_bytes"] = values["FETCH_SIZE"] * 1024.0
+            fetch = values["FETCH_SIZE"] * 1024.0 * factors.get("FETCH_SIZE", 1.0)
+            entry["dram_fetch_bytes"] = fetch
         if "WRITE_SIZE" in values:
-            entry["dram_write_bytes"] = values["WRITE_SIZE"] * 1024.0
-        if duration and "FETCH_SIZE" in values and "WRITE_SIZE" in values:
-            entry["dram_gbps"] = (values["FETCH_SIZE"] + values["WRITE_SIZE"]) * 1024.0 / duration
+            write = values["WRITE_SIZE"] * 1024.0 * factors.get("WRITE_SIZE", 1.0)
+            entry["dram_write_bytes"] = write
+        if factors:
+            entry["calibrated"] = True
+        if duration and fetch is not None and write is not None:
+            entry["dram_gbps"] = (fetch + write) / duration
         if values.get("GRBM_GUI_ACTIVE") and "SQ_VALU_MFMA_BUSY_CYCLES" in values:
-            entry["mfma_busy_pct"] = (
-                100.0 * values["SQ_VALU_MFMA_BUSY_CYCLES"] / (values["GRBM_GUI_ACTIVE"] * cus * SIMDS_PER_CU)
-            )
+            per_xcd = values["GRBM_GUI_ACTIVE"] / xcds
+            entry["mfma_busy_pct"] = 100.0 * values["SQ_VALU_MFMA_BUSY_CYCLES"] / (per_xcd * cus * SIMDS_PER_CU)
+            if duration:
+                entry["clock_ghz"] = per_xcd / duration
         summary[name] = entry
     return summary
 

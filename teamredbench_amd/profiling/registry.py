@@ -5,6 +5,8 @@ An engine turns (params, child command, artifact dir, suite dir) into a
 ``extra_passes`` are further runs of the same child under the profiler (one
 per hardware-counter group -- rocprofv3 collects a limited number of counters
 per pass) whose records are discarded and whose artifacts are parsed.
+``standalone_passes`` are complete commands run once each after those (for
+example a calibration workload of known traffic under the same counters).
 ``collect`` (optional) parses the artifact directory into a JSON-able
 summary that the runner attaches to the metadata sidecar.
 """
@@ -22,6 +24,7 @@ class ProfilingLaunch:
     env: dict[str, str] = field(default_factory=dict)
     metadata: dict[str, Any] = field(default_factory=dict)
     extra_passes: tuple[tuple[str, ...], ...] = ()
+    standalone_passes: tuple[tuple[str, ...], ...] = ()
     collect: Callable[[Path], dict[str, Any]] | None = None
 
 

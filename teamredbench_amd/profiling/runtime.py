@@ -113,6 +113,8 @@ def run_profiled_suite(*, suite: SuiteConfig, context: BenchmarkContext, output_
     for index, prefix in enumerate(launch.extra_passes):
         pass_out = artifact_dir / f"pass{index + 1}-results"
         _run([*prefix, *child_command(suite.path, device_id, pass_out)], env, f"{engine.name} pass {index + 1}")
+    for index, command in enumerate(launch.standalone_passes):
+        _run(list(command), env, f"{engine.name} standalone pass {index + 1}")
 
     profiling: dict[str, Any] = {
         "enabled": True,
@@ -120,6 +122,7 @@ def run_profiled_suite(*, suite: SuiteConfig, context: BenchmarkContext, output_
         "artifact_dir": str(launch.artifact_dir),
         "command": list(launch.command),
         "extra_passes": [list(p) for p in launch.extra_passes],
+        "standalone_passes": [list(p) for p in launch.standalone_passes],
         "engine_metadata": dict(launch.metadata),
     }
     if launch.collect is not None:

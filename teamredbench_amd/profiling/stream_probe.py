@@ -6,7 +6,7 @@ counters report. The copy launches move a known number of bytes (read n*4,
 write n*4), which calibrates the counters; the triad launches are the
 workload being measured (read 2*n*4, write n*4).
 
-    python -m teamredbench_amd.profiling.stream_probe [--elements N] [--launches K]
+    python -m teamredbench_amd.profiling.stream_probe [--elements N] [--launches K] [--ops copy,triad]
 """
 from __future__ import annotations
 
@@ -19,7 +19,11 @@ def main(argv: list[str] | None = None) -> int:
     parser = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     parser.add_argument("--elements", type=int, default=1 << 28)
     parser.add_argument("--launches", type=int, default=5)
+    parser.add_argument("--ops", default="copy,triad", help="comma-separated subset of copy,triad")
     args = parser.parse_args(argv)
+    ops = [o for o in args.ops.split(",") if o]
+    if not ops or any(o not in ("copy", "triad") for o in ops):
+        parser.error("--ops takes copy and/or triad")
 
     import torch
 
@@ -36,6 +40,8 @@ def main(argv: list[str] | None = None) -> int:
     stream = torch.cuda.current_stream().cuda_stream
     launched = {}
     for name, op in (("copy", capi.OP_COPY), ("triad", capi.OP_TRIAD)):
+        if name not in ops:
+            continue
         for _ in range(args.launches):
             lib.stream(op, capi.DT_FLOAT32, a.data_ptr(), b.data_ptr(), c.data_ptr(), n, 3.0, 0, stream)
         torch.cuda.synchronize()
