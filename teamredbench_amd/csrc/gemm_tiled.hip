@@ -22,14 +22,13 @@
 // Each keeps every operand read of a wave free of bank conflicts for both 8-
 // and 16-lane LDS phases (checked exhaustively on the host).
 //
-// Pipeline. STAGES LDS slots form a ring with one barrier per stage; the
-// loads of stage k + STAGES - 1 go out in the middle of step k, as soon as
-// every wave has finished with the slot stage k - 1 used, so about
-// STAGES - 1.5 stages of loads are in flight under the MFMAs. Each stage's
-// MFMAs run in two halves, and the LDS reads of the next half (across the
-// barrier for the next stage) overlap the MFMAs of the current one. The
-// barrier is a bare s_barrier preceded by an explicit vmcnt wait for the one
-// stage needed next -- a full __syncthreads() would wait for all of them.
+// Pipeline. STAGES LDS slots form a ring with one barrier per stage. While
+// the MFMAs of stage k run from registers, every operand of stage k + 1 is
+// read from LDS into a second register set and the loads of stage
+// k + STAGES go into the slot stage k has just vacated, all spread evenly
+// between the MFMAs; so all STAGES slots have loads in flight. The barrier
+// is a bare s_barrier preceded by an explicit vmcnt wait for the one stage
+// needed next -- a full __syncthreads() would wait for all of them.
 //
 // Waves form a WGM x WGN grid; each wave owns (BM/WGM) x (BN/WGN) of C as
 // 32 x 32 fragments: v_mfma_f32_32x32x16_{bf16,f16} (two per stage), or for
@@ -296,121 +295,116 @@ gemm_tiled_kernel(const unsigned char* __restrict__ A, const unsigned char* __re
     const int a_row = wm * WTM + (lane & 31);
     const int b_col = wn * WTN;
 
-    // Operands of half a stage. 16-bit: half p is K substep p (all fragments).
-    // fp8: the stage is one K substep; half p covers A fragments
-    // [p * FM/2, (p+1) * FM/2) and both halves use the B fragments read with
-    // half 0.
-    struct Ops {
-        Frag a[FM];
-        Frag b[FN];
+    // The operands of one stage. 16-bit: two K substeps of 16 (one MFMA per
+    // fragment pair each), one 16-byte A read and two transposing B reads per
+    // fragment and substep. fp8: one substep of 64, two A reads and four B
+    // reads per fragment.
+    constexpr bool kWide = Tr::kElem == 1;             // fp8: 32-byte operands
+    constexpr int SUBS = kWide ? 1 : 2;                 // K substeps per stage
+    constexpr int B_PIECES = kWide ? 4 : 2;             // transposing reads per B fragment
+    constexpr int A_PIECES = kWide ? 2 : 1;             // 16-byte reads per A fragment
+    constexpr int PER_SUB = FM * A_PIECES + FN * B_PIECES;
+    constexpr int N_READS = SUBS * PER_SUB;
+    constexpr int N_MFMA = SUBS * FM * FN;
+    constexpr int N_MEM = N_READS + LOADS;              // memory instructions per step
+    constexpr int PER = (N_MEM + N_MFMA - 1) / N_MFMA;  // ... issued after each MFMA
+    // Memory instruction m of a step is a load when m + 1 is one of the first
+    // LOADS multiples of kLoadStride, otherwise the next operand read: the
+    // loads sit evenly among the reads.
+    constexpr int kLoadStride = N_MEM / LOADS;
+    constexpr auto kIsLoad = [](int m) { return (m + 1) % kLoadStride == 0 && (m + 1) / kLoadStride <= LOADS; };
+    struct StageOps {
+        Frag a[SUBS][FM];
+        Frag b[SUBS][FN];
     };
-    constexpr bool kWide = Tr::kElem == 1;            // fp8: 32-byte operands
-    constexpr int FM_HALF = kWide ? FM / 2 : FM;
-    constexpr int B_PIECES = kWide ? 4 : 2;           // transposing reads per B fragment
-    constexpr int A_PIECES = kWide ? 2 : 1;           // 16-byte reads per A fragment
-    static_assert(!kWide || FM % 2 == 0, "fp8 halves split the A fragments");
-    // LDS reads that fill the operands of half P, and the MFMAs of a half.
-    constexpr int kReads0 = (kWide ? FN * B_PIECES : FN * B_PIECES) + FM_HALF * A_PIECES;
-    constexpr int kReads1 = (kWide ? 0 : FN * B_PIECES) + FM_HALF * A_PIECES;
-    constexpr int kMfmas = FM_HALF * FN;
 
-    // Read number r of half P of the stage in `slot` into o (B pieces first).
-    auto read_one = [&](const unsigned char* slot, auto part, auto idx, Ops& o) {
-        constexpr int P = decltype(part)::value;
+    // Read number r of a stage, in the order the MFMAs consume operands: per
+    // substep A fragment 0, then the B fragments, then A fragments 1..FM-1.
+    auto read_op = [&](const unsigned char* slot, auto idx, StageOps& o) {
         constexpr int r = decltype(idx)::value;
-        constexpr int nb_reads = (kWide && P == 1) ? 0 : FN * B_PIECES;
-        const unsigned char* sb = slot + A_BYTES;
-        if constexpr (r < nb_reads) {
-            constexpr int j = r / B_PIECES, t = r % B_PIECES;
-            const u32x2 v = read_b_piece<DT, BN>(sb, b_col + 32 * j, kWide ? 0 : P, t, lane);
-            o.b[j][2 * t] = v[0];
-            o.b[j][2 * t + 1] = v[1];
+        constexpr int s = r / PER_SUB, u = r % PER_SUB;
+        if constexpr (u >= A_PIECES && u < A_PIECES + FN * B_PIECES) {
+            constexpr int j = (u - A_PIECES) / B_PIECES, t = (u - A_PIECES) % B_PIECES;
+            const u32x2 v = read_b_piece<DT, BN>(slot + A_BYTES, b_col + 32 * j, s, t, lane);
+            o.b[s][j][2 * t] = v[0];
+            o.b[s][j][2 * t + 1] = v[1];
         } else {
-            constexpr int q = r - nb_reads;
-            constexpr int i = (kWide ? P * FM_HALF : 0) + q / A_PIECES, e = q % A_PIECES;
-            const int chunk = kWide ? 2 * half + e : 2 * P + half;
+            constexpr int q = u < A_PIECES ? u : u - FN * B_PIECES;
+            constexpr int i = q / A_PIECES, e = q % A_PIECES;
+            const int chunk = kWide ? 2 * half + e : 2 * s + half;
             const u32x4 v = read_a_piece(slot, a_row + 32 * i, chunk);
 #pragma unroll
-            for (int w = 0; w < 4; ++w) o.a[i][4 * e + w] = v[w];
+            for (int w = 0; w < 4; ++w) o.a[s][i][4 * e + w] = v[w];
         }
     };
-    auto mfma_one = [&](auto part, auto idx, const Ops& o) {
-        constexpr int P = decltype(part)::value;
+    auto mfma_op = [&](auto idx, const StageOps& o) {
         constexpr int q = decltype(idx)::value;
-        constexpr int i = (kWide ? P * FM_HALF : 0) + q / FN, j = q % FN;
-        acc[i][j] = Tr::mfma(o.b[j], o.a[i], acc[i][j]);
-    };
-    using Half0 = std::integral_constant<int, 0>;
-    using Half1 = std::integral_constant<int, 1>;
-
-    // Runs the MFMAs of one half with `nmem` memory operations spread evenly
-    // between them (front-loaded: ceil(nmem / MFMAs) after each MFMA);
-    // sched_barrier(0) pins the order so the MFMA pipe never waits on a burst
-    // of issues.
-    auto interleave = [&](auto part, const Ops& o, auto nmem, auto&& mem) {
-        constexpr int N_MEM = decltype(nmem)::value;
-        constexpr int PER = (N_MEM + kMfmas - 1) / kMfmas;
-        [&]<int... Q>(std::integer_sequence<int, Q...>) {
-            ([&] {
-                mfma_one(part, std::integral_constant<int, Q>{}, o);
-                constexpr int lo = Q * PER < N_MEM ? Q * PER : N_MEM;
-                constexpr int hi = Q * PER + PER < N_MEM ? Q * PER + PER : N_MEM;
-                [&]<int... R>(std::integer_sequence<int, R...>) {
-                    (mem(std::integral_constant<int, lo + R>{}), ...);
-                }(std::make_integer_sequence<int, hi - lo>{});
-                __builtin_amdgcn_sched_barrier(0);
-            }(), ...);
-        }(std::make_integer_sequence<int, kMfmas>{});
+        constexpr int s = q / (FM * FN), i = (q / FN) % FM, j = q % FN;
+        acc[i][j] = Tr::mfma(o.b[s][j], o.a[s][i], acc[i][j]);
     };
 
     // Software pipeline over a ring of STAGES slots, one barrier per stage:
-    //   step kt (stage kt in slot kt % STAGES, its half-0 operands in `next`):
-    //     MFMAs of half 0, with the LDS reads of half 1 of stage kt between them
-    //     wait for this wave's loads of stage kt+1, barrier
-    //     MFMAs of half 1, with the LDS reads of half 0 of stage kt+1 and the
-    //     loads of stage kt+STAGES-1 (into the slot stage kt-1 used) between them
-    // The barrier certifies stage kt+1 for every wave and that every wave is
-    // done reading slot kt-1 (those reads fed MFMAs before the barrier).
-    // Loads past the last stage re-read the last stage (in bounds, never
-    // consumed), so every step issues the same number of loads and the vmcnt
-    // bookkeeping stays uniform. The loop is unrolled by STAGES so every slot
-    // is a compile-time choice.
+    //   step kt (stage kt in slot kt % STAGES, its operands already in
+    //   registers):
+    //     wait for this wave's loads of stage kt+1 and its LDS reads, barrier
+    //     the stage's MFMAs, with the LDS reads of all of stage kt+1 (into the
+    //     other register set) and the loads of stage kt+STAGES (into slot kt)
+    //     spread evenly between them
+    // The barrier certifies stage kt+1 for every wave, and that every wave has
+    // finished reading slot kt (those reads went out during step kt-1), so all
+    // STAGES slots hold loads in flight. Loads past the last stage re-read the
+    // last stage (in bounds, never consumed), so every step issues the same
+    // number of loads and the vmcnt bookkeeping stays uniform.
+    // sched_barrier(0) after each MFMA and its memory instructions pins the
+    // interleaving, so the MFMA pipe never waits behind a burst of issues.
     const int ksteps = k_len / K_ROWS;
     const int last = ksteps - 1;
     [&]<int... P>(std::integer_sequence<int, P...>) {
         (issue_stage(min(P, last), slot_ptr(std::integral_constant<int, P>{})), ...);
-    }(std::make_integer_sequence<int, STAGES - 1>{});
-    Ops next;
-    wait_vmcnt_and_barrier<LOADS * (STAGES - 2)>();
+    }(std::make_integer_sequence<int, STAGES>{});
+    // Two operand sets, used alternately (step I computes from set I % 2 and
+    // reads into the other); the loop is unrolled to an even number of steps
+    // that is also a multiple of STAGES, so every slot is a compile-time
+    // choice and the sets are never copied.
+    StageOps ops[2];
+    wait_vmcnt_and_barrier<LOADS * (STAGES - 1)>();
     [&]<int... R>(std::integer_sequence<int, R...>) {
-        (read_one(slot_ptr(std::integral_constant<int, 0>{}), Half0{}, std::integral_constant<int, R>{}, next), ...);
-    }(std::make_integer_sequence<int, kReads0>{});
+        (read_op(slot_ptr(std::integral_constant<int, 0>{}), std::integral_constant<int, R>{}, ops[0]), ...);
+    }(std::make_integer_sequence<int, N_READS>{});
 
     auto step = [&](auto idx, int kt) {
         constexpr int I = decltype(idx)::value;
-        const unsigned char* cur_slot = slot_ptr(idx);
         const unsigned char* next_slot = slot_ptr(std::integral_constant<int, (I + 1) % STAGES>{});
-        unsigned char* load_slot = slot_ptr(std::integral_constant<int, (I + STAGES - 1) % STAGES>{});
-        const Ops cur0 = next;
-        Ops cur1 = cur0;  // fp8 keeps the B fragments of half 0
-        interleave(Half0{}, cur0, std::integral_constant<int, kReads1>{},
-                   [&](auto r) { read_one(cur_slot, Half1{}, r, cur1); });
-        wait_vmcnt_and_barrier<LOADS * (STAGES - 3)>();
-        const int kload = min(kt + STAGES - 1, last);
-        // Operand reads first (they feed the next MFMAs), the loads after them.
-        interleave(Half1{}, cur1, std::integral_constant<int, LOADS + kReads0>{}, [&](auto m) {
-            constexpr int q = decltype(m)::value;
-            if constexpr (q < kReads0) {
-                read_one(next_slot, Half0{}, std::integral_constant<int, q>{}, next);
-            } else {
-                issue_one(kload, load_slot, std::integral_constant<int, q - kReads0>{});
-            }
-        });
+        unsigned char* load_slot = slot_ptr(std::integral_constant<int, I % STAGES>{});
+        const StageOps& cur = ops[I % 2];
+        StageOps& nxt = ops[(I + 1) % 2];
+        wait_vmcnt_and_barrier<LOADS * (STAGES - 2)>();
+        const int kload = min(kt + STAGES, last);
+        [&]<int... Q>(std::integer_sequence<int, Q...>) {
+            ([&] {
+                mfma_op(std::integral_constant<int, Q>{}, cur);
+                constexpr int lo = Q * PER < N_MEM ? Q * PER : N_MEM;
+                constexpr int hi = Q * PER + PER < N_MEM ? Q * PER + PER : N_MEM;
+                [&]<int... R>(std::integer_sequence<int, R...>) {
+                    ([&] {
+                        constexpr int m = lo + R;
+                        if constexpr (kIsLoad(m)) {
+                            issue_one(kload, load_slot, std::integral_constant<int, (m + 1) / kLoadStride - 1>{});
+                        } else {
+                            constexpr int loads_before = m / kLoadStride < LOADS ? m / kLoadStride : LOADS;
+                            read_op(next_slot, std::integral_constant<int, m - loads_before>{}, nxt);
+                        }
+                    }(), ...);
+                }(std::make_integer_sequence<int, hi - lo>{});
+                __builtin_amdgcn_sched_barrier(0);
+            }(), ...);
+        }(std::make_integer_sequence<int, N_MFMA>{});
     };
-    for (int kt = 0; kt < ksteps; kt += STAGES) {
+    constexpr int UNROLL = STAGES % 2 ? 2 * STAGES : STAGES;
+    for (int kt = 0; kt < ksteps; kt += UNROLL) {
         [&]<int... I>(std::integer_sequence<int, I...>) {
             ((kt + I < ksteps ? step(std::integral_constant<int, I>{}, kt + I) : void()), ...);
-        }(std::make_integer_sequence<int, STAGES>{});
+        }(std::make_integer_sequence<int, UNROLL>{});
     }
     wait_vmcnt_and_barrier<0>();
 
@@ -535,7 +529,7 @@ int gemm_tiled_plan(int dtype, int64_t M, int64_t N, int64_t K, const DeviceProp
     // K splits for problems with too few tiles to fill the GPU, as long as the
     // fp32 partials (splits * M * N * 4 bytes) stay small next to B's bytes.
     int splits = 1;
-    if (cfg == 1) {
+    if (kConfigs[cfg].bm == 128) {
         while (tiles(cfg) * splits * 2 <= 2 * cus && K % (stage_k * splits * 2) == 0 &&
                2 * splits * M * 4 <= K * e / 4)
             splits *= 2;
