@@ -34,7 +34,8 @@
 // 32 x 32 fragments: v_mfma_f32_32x32x16_{bf16,f16} (two per stage), or for
 // fp8 v_mfma_f32_32x32x64_f8f6f4 (one per stage). The MFMA takes the B
 // fragment as its first operand, so a lane's 16 accumulators are 4 runs of 4
-// consecutive C columns in one C row: the epilogue stores 8 bytes at a time.
+// consecutive C columns in one C row. The epilogue rounds them to 16 bits
+// through LDS so that the stores to C are whole 256-byte row segments.
 //
 // Tile order: blocks are dispatched round-robin over the 8 XCDs (block b on
 // XCD b % 8); each XCD gets a contiguous range of tiles in an order grouped
@@ -409,18 +410,32 @@ gemm_tiled_kernel(const unsigned char* __restrict__ A, const unsigned char* __re
     wait_vmcnt_and_barrier<0>();
 
     // Epilogue. Accumulator register r = 4g + q of lane l holds
-    // C[row = 32*i + l % 32][col = 32*j + 8g + 4*(l / 32) + q]. Rows at or past
-    // M (a partial last tile) are not stored. With K splits the block writes
-    // its unscaled fp32 partial to ws[split][row][col]; a second kernel sums
-    // the splits.
+    // C[row = 32*i + l % 32][col = 32*j + 8g + 4*(l / 32) + q]: stored straight
+    // from registers, every store instruction would put 16 bytes into each of
+    // 32 rows. Instead each wave rounds its (WTM x WTN) tile to 16 bits into
+    // the LDS slot with its own index (every slot is free after the final
+    // barrier), then reads it back row by row so that 16 lanes store one
+    // 256-byte row segment: whole cache lines, half the store instructions.
+    // Staged rows are 16 chunks of 16 bytes; chunk c of row r sits at chunk
+    // c ^ (r % 16), which keeps both the writes (32 rows, one chunk) and the
+    // reads (4 rows, all chunks) free of bank conflicts. Rows at or past M (a
+    // partial last tile) are not stored. With K splits the block writes its
+    // unscaled fp32 partial to ws[split][row][col] directly; a second kernel
+    // sums the splits.
     const int row0 = tm * BM + wm * WTM + (lane & 31);
     const int64_t col0 = (int64_t)tn * BN + wn * WTN + 4 * half;
     if (ws == nullptr) {
-        const int64_t ldc = (int64_t)N * 2;  // bytes per C row (16-bit output)
+        constexpr int ROW_BYTES = WTN * 2;
+        constexpr int ROW_CHUNKS = ROW_BYTES / 16;
+        static_assert(ROW_CHUNKS == 16, "staging swizzle assumes 256-byte rows");
+        static_assert(WTM * ROW_BYTES <= SLOT && W <= STAGES, "a wave's tile must fit its slot");
+        unsigned char* stage = wave == 0   ? slot_ptr(std::integral_constant<int, 0>{})
+                               : wave == 1 ? slot_ptr(std::integral_constant<int, 1>{})
+                               : wave == 2 ? slot_ptr(std::integral_constant<int, 2>{})
+                                           : slot_ptr(std::integral_constant<int, 3>{});
 #pragma unroll
         for (int i = 0; i < FM; ++i) {
-            if (row0 + 32 * i >= M) continue;
-            unsigned char* crow = C + (int64_t)(row0 + 32 * i) * ldc;
+            const int r = 32 * i + (lane & 31);
 #pragma unroll
             for (int j = 0; j < FN; ++j) {
 #pragma unroll
@@ -428,9 +443,24 @@ gemm_tiled_kernel(const unsigned char* __restrict__ A, const unsigned char* __re
                     const f32x16& v = acc[i][j];
                     const u32x2 packed = pack4<DT>(v[4 * g] * alpha, v[4 * g + 1] * alpha, v[4 * g + 2] * alpha,
                                                    v[4 * g + 3] * alpha);
-                    *reinterpret_cast<u32x2*>(crow + (col0 + 32 * j + 8 * g) * 2) = packed;
+                    const int chunk = (4 * j + g) ^ (r % ROW_CHUNKS);
+                    *reinterpret_cast<u32x2*>(stage + r * ROW_BYTES + chunk * 16 + 8 * half) = packed;
                 }
             }
+        }
+        const int64_t ldc = (int64_t)N * 2;  // bytes per C row (16-bit output)
+        constexpr int ROWS_PER_STORE = 64 / ROW_CHUNKS;
+        const int c = lane % ROW_CHUNKS;
+        const int r0 = lane / ROW_CHUNKS;
+        int grow = tm * BM + wm * WTM + r0;
+        unsigned char* cptr = C + (int64_t)grow * ldc + ((int64_t)tn * BN + wn * WTN) * 2 + c * 16;
+#pragma unroll
+        for (int p = 0; p < WTM / ROWS_PER_STORE; ++p) {
+            const int r = ROWS_PER_STORE * p + r0;
+            const u32x4 v = *reinterpret_cast<const u32x4*>(stage + r * ROW_BYTES + ((c ^ (r % ROW_CHUNKS)) << 4));
+            if (grow < M) *reinterpret_cast<u32x4*>(cptr) = v;
+            grow += ROWS_PER_STORE;
+            cptr += ROWS_PER_STORE * ldc;
         }
     } else {
         float* part = ws + (int64_t)split * M * N;
@@ -469,7 +499,7 @@ struct TiledConfig {
 };
 
 constexpr TiledConfig kConfigs[] = {
-    {256, 256, 2, 2, 5, 8},  // 0: large problems, 128 x 128 per wave, 5 x 32 KiB stages
+    {256, 256, 2, 2, 5, 4},  // 0: large problems, 128 x 128 per wave, 5 x 32 KiB stages
     {128, 256, 2, 2, 6, 8},  // 1: mid-size problems, 64 x 128 per wave, 6 x 24 KiB stages
 };
 constexpr int kNumConfigs = sizeof(kConfigs) / sizeof(kConfigs[0]);
