@@ -165,6 +165,22 @@ def parse_counters(pmc_dir: Path) -> dict[str, dict[str, float]]:
     return {k: {c: mean(v) for c, v in counters.items()} for k, counters in grouped.items()}
 
 
+def parse_counter_durations(pmc_dir: Path) -> dict[str, float]:
+    """kernel name -> mean dispatch duration (ns) of a counter-collection run,
+    from the Start/End timestamps rocprofv3 records with every counter row."""
+    spans: dict[tuple[str, str], int] = {}
+    for row in _rows(sorted(pmc_dir.rglob("*counter_collection.csv"))):
+        try:
+            span = int(row["End_Timestamp"]) - int(row["Start_Timestamp"])
+        except (KeyError, ValueError):
+            continue
+        spans[(_kernel_name(row), row.get("Dispatch_Id", "?"))] = span
+    grouped: dict[str, list[int]] = {}
+    for (kernel, _), span in spans.items():
+        grouped.setdefault(kernel, []).append(span)
+    return {k: mean(v) for k, v in grouped.items()}
+
+
 def calibration_factors(artifact_dir: Path) -> dict[str, float]:
     """FETCH_SIZE / WRITE_SIZE scale factors from the calibration passes:
     known bytes of the copy kernel / (counter KiB * 1024)."""
@@ -188,9 +204,14 @@ def collect(artifact_dir: Path, cu_count: int | None = None, xcd_count: int | No
     """Per-kernel summary from a rocprofv3 artifact directory (trace + pmc passes)."""
     kernels = parse_kernel_trace(artifact_dir / "trace") if (artifact_dir / "trace").exists() else {}
     counters: dict[str, dict[str, float]] = {}
+    gui_durations: dict[str, float] = {}   # durations of the runs that read GRBM_GUI_ACTIVE
     for pmc_dir in sorted(artifact_dir.glob("pmc*")):
-        for kernel, values in parse_counters(pmc_dir).items():
+        parsed = parse_counters(pmc_dir)
+        durations = parse_counter_durations(pmc_dir)
+        for kernel, values in parsed.items():
             counters.setdefault(kernel, {}).update(values)
+            if "GRBM_GUI_ACTIVE" in values and kernel in durations:
+                gui_durations[kernel] = durations[kernel]
     cus = cu_count or int(os.environ.get("MB_CU_COUNT", "256"))
     xcds = xcd_count or int(os.environ.get("MB_XCD_COUNT", "8"))
     factors = calibration_factors(artifact_dir)
@@ -214,8 +235,11 @@ def collect(artifact_dir: Path, cu_count: int | None = None, xcd_count: int | No
         if values.get("GRBM_GUI_ACTIVE") and "SQ_VALU_MFMA_BUSY_CYCLES" in values:
             per_xcd = values["GRBM_GUI_ACTIVE"] / xcds
             entry["mfma_busy_pct"] = 100.0 * values["SQ_VALU_MFMA_BUSY_CYCLES"] / (per_xcd * cus * SIMDS_PER_CU)
-            if duration:
-                entry["clock_ghz"] = per_xcd / duration
+            # the clock comes from the same run as the cycle count when that
+            # run recorded timestamps, else from the trace run
+            clock_span = gui_durations.get(name) or duration
+            if clock_span:
+                entry["clock_ghz"] = per_xcd / clock_span
         summary[name] = entry
     return summary
 

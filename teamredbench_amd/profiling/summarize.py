@@ -11,10 +11,11 @@
         and write exactly its known bytes; prints a `traffic_bytes_per_launch:`
         line that bench.py reads.
 
-    python -m teamredbench_amd.profiling.summarize mfma <dir> --kernel <regex> [--duration-us T]
+    python -m teamredbench_amd.profiling.summarize mfma <dir> --kernel <regex> [--duration-us T ...]
         SQ_VALU_MFMA_BUSY_CYCLES against GRBM_GUI_ACTIVE (summed over the
         XCDs) for each matching kernel: the fraction of SIMD cycles the MFMA
-        units were busy, and, given the kernel's duration, the clock it ran at.
+        units were busy, and the clock it ran at over the dispatch duration
+        (the counter run's own timestamps unless --duration-us is given).
 
 The directories are rocprofv3 output directories written with `-f csv`.
 """
@@ -26,7 +27,7 @@ from pathlib import Path
 import re
 import sys
 
-from teamredbench_amd.profiling.builtin import parse_counters
+from teamredbench_amd.profiling.builtin import parse_counter_durations, parse_counters
 
 
 def _kernel_stats(directory: Path) -> list[dict[str, str]]:
@@ -93,6 +94,7 @@ def mfma(directory: Path, kernel: str, durations_us: list[float], xcds: int, cus
     counters = {k: v for k, v in parse_counters(directory).items() if rx.search(k)}
     if not counters:
         raise SystemExit(f"no kernel matching {kernel!r} under {directory}")
+    own = parse_counter_durations(directory)
     lines = []
     for idx, (name, values) in enumerate(sorted(counters.items())):
         busy, gui = values.get("SQ_VALU_MFMA_BUSY_CYCLES"), values.get("GRBM_GUI_ACTIVE")
@@ -103,9 +105,12 @@ def mfma(directory: Path, kernel: str, durations_us: list[float], xcds: int, cus
             per_xcd = gui / xcds
             lines.append(f"  mfma_busy_pct (busy / (GUI_ACTIVE/{xcds} * {cus} CUs * 4 SIMDs)): "
                          f"{100.0 * busy / (per_xcd * cus * 4):.2f}")
-            if idx < len(durations_us):
+            span_us = durations_us[idx] if idx < len(durations_us) else own.get(name, 0.0) / 1e3
+            if span_us:
+                source = "given" if idx < len(durations_us) else "this run's timestamps"
+                lines.append(f"  average dispatch duration ({source}): {span_us:.2f} us")
                 lines.append(f"  clock over the dispatch (GUI_ACTIVE/{xcds} / duration): "
-                             f"{per_xcd / durations_us[idx] / 1e3:.3f} GHz")
+                             f"{per_xcd / span_us / 1e3:.3f} GHz")
     return "\n".join(lines)
 
 
