@@ -52,6 +52,7 @@ extern "C" {
 #define MB_DT_FLOAT64 3
 #define MB_DT_INT8 4           /* copy only */
 #define MB_DT_FLOAT8_E4M3FN 5  /* GEMM inputs only; output is bfloat16 */
+#define MB_DT_FLOAT8_E5M2 6    /* GEMM inputs only; output is bfloat16 */
 
 /* Kinds for mb_kernel_info. */
 #define MB_KIND_STREAM 0
@@ -95,14 +96,21 @@ int mb_time_stream(int op, int dtype, void* dst, const void* b, const void* c,
  * pack_b_tiles_kernel<T> pre-pass (:396-409): B is consumed as given,
  * row-major K x N, with no re-layout outside the timed kernel.
  *
- * dtype  A (M x K)   B (K x N)   C (M x N)   epilogue
- * BF16   bf16        bf16        bf16        RNE(acc)
- * F16    fp16        fp16        fp16        RNE(acc)
- * FP8    e4m3fn      e4m3fn      bf16        RNE(scale_a * scale_b * acc)
+ * dtype        A (M x K)   B (K x N)   C (M x N)   accumulate / epilogue
+ * BFLOAT16     bf16        bf16        bf16        fp32 / RNE(acc)
+ * FLOAT16      fp16        fp16        fp16        fp32 / RNE(acc)
+ * FLOAT8_E4M3FN e4m3fn     e4m3fn      bf16        fp32 / RNE(scale_a * scale_b * acc)
+ * FLOAT8_E5M2  e5m2        e5m2        bf16        fp32 / RNE(scale_a * scale_b * acc)
+ * FLOAT32      fp32        fp32        fp32        fp32 MFMA (full precision)
+ * FLOAT64      fp64        fp64        fp64        fp64 MFMA
  * scale_a/scale_b are the fp8 per-tensor dequantisation scales (ignored for
- * bf16/f16). Leading dimensions are K, N and N. Any M, N, K >= 1 whose rows
- * keep 16-byte alignment (K*elem and N*elem multiples of 16) with 16-byte
- * aligned base pointers; other shapes return MB_ERR_SHAPE.
+ * the other types). Leading dimensions are K, N and N. Any M, N, K >= 1 with
+ * 16-byte aligned base pointers; shapes the pipelined kernels do not divide
+ * (16-bit and fp8: N % 256, K % 64 bytes) run on bounds-checked kernels.
+ * FLOAT32 / FLOAT64 follow the reference's high-precision path
+ * (mfu_gemm_highp.hip.hpp:39-218) on v_mfma_f32_32x32x2_f32 and
+ * v_mfma_f64_16x16x4_f64; FLOAT8_E5M2 is the dtype the reference declares
+ * (dtypes.py:24) but does not run natively (mfu_gemm.hip.cpp:9-21).
  * workspace: device scratch of at least mb_gemm_workspace_size() bytes (may
  * be NULL when that size is 0). The kernels leave it in a state the next
  * call can use without clearing.

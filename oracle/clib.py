@@ -33,7 +33,7 @@ def load() -> ctypes.CDLL:
         lib.oracle_stream.restype = ctypes.c_int
         lib.oracle_stream.argtypes = [ctypes.c_int, ctypes.c_int, vp, vp, vp, u64, ctypes.c_double]
         for name in ("oracle_decode_bf16", "oracle_encode_bf16", "oracle_decode_f16", "oracle_encode_f16",
-                     "oracle_decode_e4m3"):
+                     "oracle_decode_e4m3", "oracle_decode_e5m2"):
             fn = getattr(lib, name)
             fn.restype = None
             fn.argtypes = [vp, vp, u64]
@@ -99,6 +99,13 @@ def decode_e4m3(codes: np.ndarray) -> np.ndarray:
     codes = np.ascontiguousarray(codes, dtype=np.uint8)
     out = np.empty(codes.shape, dtype=np.float32)
     load().oracle_decode_e4m3(_ptr(codes), _ptr(out), codes.size)
+    return out
+
+
+def decode_e5m2(codes: np.ndarray) -> np.ndarray:
+    codes = np.ascontiguousarray(codes, dtype=np.uint8)
+    out = np.empty(codes.shape, dtype=np.float32)
+    load().oracle_decode_e5m2(_ptr(codes), _ptr(out), codes.size)
     return out
 
 

@@ -29,9 +29,12 @@ TORCH_DTYPES = {
     "float64": torch.float64,
     "int8": torch.int8,
     "float8_e4m3fn": torch.float8_e4m3fn,
+    "float8_e5m2": torch.float8_e5m2,
 }
 
 FP8_E4M3_MAX = 448.0
+FP8_E5M2_MAX = 57344.0
+FP8_MAX = {"float8_e4m3fn": FP8_E4M3_MAX, "float8_e5m2": FP8_E5M2_MAX}
 
 
 # ---------------------------------------------------------------- stream path
@@ -79,19 +82,19 @@ def stream_inputs(n: int, dtype: str, seed: int = 0) -> tuple[torch.Tensor, torc
 def gemm_inputs(m: int, n: int, k: int, dtype: str, seed: int = 0) -> dict:
     """Seeded GEMM operands as CPU tensors.
 
-    bfloat16 / float16: A (m x k) ~ normal(0, 1/sqrt(k)) from seed, B (k x n)
-    from seed + 1, drawn in fp32 and cast.
-    float8_e4m3fn: A, B ~ normal(0, 1) from the same seeds; each is scaled so
-    its amax maps to 448 and cast to e4m3fn; scale_a / scale_b are the
-    dequantisation factors amax / 448.
+    bfloat16 / float16 / float32 / float64: A (m x k) ~ normal(0, 1/sqrt(k))
+    from seed, B (k x n) from seed + 1, drawn in fp32 and cast.
+    float8_e4m3fn / float8_e5m2: A, B ~ normal(0, 1) from the same seeds; each
+    is scaled so its amax maps to the format's largest finite value (448,
+    57344) and cast; scale_a / scale_b are the dequantisation factors.
     """
     ga = torch.Generator().manual_seed(seed)
     gb = torch.Generator().manual_seed(seed + 1)
     a32 = torch.randn(m, k, generator=ga, dtype=torch.float32)
     b32 = torch.randn(k, n, generator=gb, dtype=torch.float32)
-    if dtype == "float8_e4m3fn":
-        qa, sa = quantize_fp8(a32)
-        qb, sb = quantize_fp8(b32)
+    if dtype in FP8_MAX:
+        qa, sa = quantize_fp8(a32, dtype)
+        qb, sb = quantize_fp8(b32, dtype)
         return {"a": qa, "b": qb, "scale_a": sa, "scale_b": sb}
     std = 1.0 / math.sqrt(k)
     return {
@@ -102,20 +105,24 @@ def gemm_inputs(m: int, n: int, k: int, dtype: str, seed: int = 0) -> dict:
     }
 
 
-def quantize_fp8(x: torch.Tensor) -> tuple[torch.Tensor, float]:
-    """Per-tensor e4m3fn quantisation with amax -> 448; returns (q, scale) with x ~= q * scale."""
+def quantize_fp8(x: torch.Tensor, dtype: str = "float8_e4m3fn") -> tuple[torch.Tensor, float]:
+    """Per-tensor fp8 quantisation with amax -> the format's largest finite
+    value; returns (q, scale) with x ~= q * scale."""
     amax = float(x.abs().max())
-    scale = amax / FP8_E4M3_MAX if amax > 0 else 1.0
-    q = (x / scale).to(torch.float8_e4m3fn)
+    scale = amax / FP8_MAX[dtype] if amax > 0 else 1.0
+    q = (x / scale).to(TORCH_DTYPES[dtype])
     return q, scale
 
 
 def gemm_reference(a: torch.Tensor, b: torch.Tensor, scale_a: float = 1.0, scale_b: float = 1.0,
                    rows: torch.Tensor | None = None) -> torch.Tensor:
-    """fp32 CPU matmul of the dequantised operands (mfu.py:234 with fp32 accumulation).
+    """fp32 CPU matmul of the dequantised operands (mfu.py:234 with fp32
+    accumulation); fp64 operands are multiplied in fp64.
 
     `rows` optionally restricts the check to a subset of C's rows (large shapes).
     """
+    if a.dtype == torch.float64:
+        return (a if rows is None else a[rows]) @ b
     af = a.float()
     if rows is not None:
         af = af[rows]
@@ -128,7 +135,8 @@ def gemm_reference(a: torch.Tensor, b: torch.Tensor, scale_a: float = 1.0, scale
 
 
 def gemm_output_dtype(dtype: str) -> torch.dtype:
-    return torch.float16 if dtype == "float16" else torch.bfloat16
+    """C's element type: fp8 inputs produce bf16, the others their own type."""
+    return {"float16": torch.float16, "float32": torch.float32, "float64": torch.float64}.get(dtype, torch.bfloat16)
 
 
 # ---------------------------------------------------------------- comparators

@@ -94,6 +94,24 @@ float oracle_e4m3_decode(uint8_t q) {
     return sign ? -v : v;
 }
 
+/* OCP bf8 e5m2: 1 sign, 5 exponent (bias 15), 2 mantissa bits; IEEE-like,
+ * with exponent 31 holding inf (mantissa 0) and NaN. */
+float oracle_e5m2_decode(uint8_t q) {
+    const int sign = q >> 7;
+    const int exp = (q >> 2) & 0x1f;
+    const int man = q & 3;
+    float v;
+    if (exp == 0x1f) {
+        if (man != 0) return sign ? -NAN : NAN;
+        v = INFINITY;
+    } else if (exp == 0) {
+        v = (float)man * 0x1p-16f;
+    } else {
+        v = ldexpf(1.0f + (float)man / 4.0f, exp - 15);
+    }
+    return sign ? -v : v;
+}
+
 void oracle_decode_bf16(const uint16_t* in, float* out, uint64_t n) {
     for (uint64_t i = 0; i < n; ++i) out[i] = oracle_bf16_decode(in[i]);
 }
@@ -108,6 +126,9 @@ void oracle_encode_f16(const float* in, uint16_t* out, uint64_t n) {
 }
 void oracle_decode_e4m3(const uint8_t* in, float* out, uint64_t n) {
     for (uint64_t i = 0; i < n; ++i) out[i] = oracle_e4m3_decode(in[i]);
+}
+void oracle_decode_e5m2(const uint8_t* in, float* out, uint64_t n) {
+    for (uint64_t i = 0; i < n; ++i) out[i] = oracle_e5m2_decode(in[i]);
 }
 
 /* Returns 0, or -1 for an unsupported (op, dtype). */

@@ -15,9 +15,10 @@ backend "native" with a built-in kernel calls libmi355bench.so (mb_time_gemm,
 event-timed on torch's current stream). B is consumed row-major as given:
 unlike the reference executable there is no untimed re-layout of B
 (native/kernels/mfu_gemm_lowp.hip.hpp:396-409). Inputs are seeded:
-bf16/fp16 ~ normal(0, 1/sqrt(k)); fp8 e4m3fn ~ normal(0, 1) quantised per
-tensor with amax -> 448, bf16 output with the dequantisation scales applied
-in the fp32 epilogue.
+bf16/fp16/fp32/fp64 ~ normal(0, 1/sqrt(k)); fp8 e4m3fn / e5m2 ~ normal(0, 1)
+quantised per tensor with amax -> the format's largest finite value (448 /
+57344), bf16 output with the dequantisation scales applied in the fp32
+epilogue. fp32 and fp64 produce C in their own type.
 """
 from __future__ import annotations
 
@@ -141,7 +142,7 @@ class MfuBenchmark(Benchmark):
                    verify_rows) -> BenchmarkRecord:
         device = self.device
         a, b, sa, sb = seeded_gemm_operands(torch, m, n, k, spec.name, device, seed)
-        out_dtype = torch.float16 if spec.name == "float16" else torch.bfloat16
+        out_dtype = getattr(torch, capi.GEMM_OUTPUT_DTYPES[spec.name])
         c = torch.empty((m, n), device=device, dtype=out_dtype)
         dt = capi.DTYPES[spec.name]
         ws_bytes = lib.gemm_workspace_size(dt, m, n, k)
@@ -150,15 +151,20 @@ class MfuBenchmark(Benchmark):
         elapsed = lib.time_gemm(dt, a.data_ptr(), b.data_ptr(), c.data_ptr(), m, n, k, sa, sb,
                                 ws.data_ptr() if ws is not None else None, ws_bytes, warmup, iterations, stream)
         meta = {**meta, **lib.gemm_info(dt, m, n, k)}
-        if spec.name == "float8_e4m3fn":
+        if spec.name in capi.FP8_DTYPES:
             meta["scale_a"], meta["scale_b"] = sa, sb
         in_bytes = spec.bytes_per_element
         moved = gemm_bytes(m, n, k, in_bytes, c.element_size())
         meta["cache_resident_b"] = k * n * in_bytes <= INFINITY_CACHE_BYTES
         if verify:
             rows = min(m, verify_rows)
-            ref = (a[:rows].float() * sa) @ (b.float() * sb)
-            meta["parity"] = gemm_parity(torch, spec.name, c[:rows].float(), ref)
+            if spec.name == "float64":
+                ref = a[:rows] @ b
+                got = c[:rows]
+            else:
+                ref = (a[:rows].float() * sa) @ (b.float() * sb)
+                got = c[:rows].float()
+            meta["parity"] = gemm_parity(torch, spec.name, got, ref)
             meta["parity"]["rows_checked"] = rows
             del ref
         return self.emit_record(

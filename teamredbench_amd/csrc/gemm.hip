@@ -8,8 +8,10 @@ namespace mb {
 
 int gemm_plan(int dtype, int64_t M, int64_t N, int64_t K, const DeviceProps& props,
               GemmPlan* plan) {
-    if (dtype != MB_DT_BFLOAT16 && dtype != MB_DT_FLOAT16 && dtype != MB_DT_FLOAT8_E4M3FN) {
-        set_error("GEMM supports bfloat16, float16 and float8_e4m3fn (got %s)", dtype_name(dtype));
+    if (dtype != MB_DT_BFLOAT16 && dtype != MB_DT_FLOAT16 && !is_fp8(dtype) && dtype != MB_DT_FLOAT32 &&
+        dtype != MB_DT_FLOAT64) {
+        set_error("GEMM supports bfloat16, float16, float8_e4m3fn, float8_e5m2, float32 and float64 (got %s)",
+                  dtype_name(dtype));
         return MB_ERR_UNSUPPORTED;
     }
     if (M < 1 || N < 1 || K < 1) {
@@ -17,6 +19,7 @@ int gemm_plan(int dtype, int64_t M, int64_t N, int64_t K, const DeviceProps& pro
                   (long long)K);
         return MB_ERR_INVALID_ARG;
     }
+    if (dtype == MB_DT_FLOAT32 || dtype == MB_DT_FLOAT64) return gemm_highp_plan(dtype, M, N, K, plan);
     if (std::getenv("MB_GEMM_FORCE_GENERIC") == nullptr &&
         gemm_tiled_plan(dtype, M, N, K, props, plan) == MB_OK)
         return MB_OK;
@@ -26,12 +29,14 @@ int gemm_plan(int dtype, int64_t M, int64_t N, int64_t K, const DeviceProps& pro
 int gemm_launch(int dtype, const void* A, const void* B, void* C, int64_t M, int64_t N, int64_t K,
                 float scale_a, float scale_b, void* workspace, const GemmPlan& plan,
                 hipStream_t stream) {
-    const float alpha = dtype == MB_DT_FLOAT8_E4M3FN ? scale_a * scale_b : 1.0f;
+    const float alpha = is_fp8(dtype) ? scale_a * scale_b : 1.0f;
     switch (plan.variant) {
         case kVariantGeneric:
             return gemm_generic_launch(dtype, A, B, C, M, N, K, alpha, stream);
         case kVariantTiled:
             return gemm_tiled_launch(dtype, A, B, C, M, N, K, alpha, workspace, plan, stream);
+        case kVariantHighp:
+            return gemm_highp_launch(dtype, A, B, C, M, N, K, stream);
         default:
             set_error("GEMM plan variant %d not available", plan.variant);
             return MB_ERR_UNSUPPORTED;

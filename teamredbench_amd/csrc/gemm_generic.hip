@@ -17,8 +17,8 @@ constexpr int kGenThreads = 256;
 
 // bf16 / f16: v_mfma_f32_16x16x32_{bf16,f16}; lane l holds row (l % 16) and
 // k-slots 8*(l/16) .. 8*(l/16)+7 of a 16 x 32 operand fragment.
-// fp8 e4m3: v_mfma_scale_f32_16x16x128_f8f6f4 with unit E8M0 scales; lane l
-// holds row (l % 16) and 32 k-slots starting at 32*(l/16).
+// fp8 (e4m3 or e5m2): v_mfma_scale_f32_16x16x128_f8f6f4 with unit E8M0
+// scales; lane l holds row (l % 16) and 32 k-slots starting at 32*(l/16).
 template <int DT>
 struct GenericTraits;
 
@@ -40,6 +40,8 @@ struct GenericTraits<MB_DT_FLOAT8_E4M3FN> {
     static constexpr int kBK = 128;
     static constexpr int kLaneK = 32;
 };
+template <>
+struct GenericTraits<MB_DT_FLOAT8_E5M2> : GenericTraits<MB_DT_FLOAT8_E4M3FN> {};
 
 template <int DT>
 __global__ void __launch_bounds__(kGenThreads)
@@ -126,14 +128,14 @@ int gemm_generic_plan(int dtype, int64_t M, int64_t N, int64_t K, GemmPlan* plan
     plan->grid = (int)(gx * gy);
     plan->tile_m = kGenTile;
     plan->tile_n = kGenTile;
-    plan->tile_k = dtype == MB_DT_FLOAT8_E4M3FN ? 128 : 32;
+    plan->tile_k = is_fp8(dtype) ? 128 : 32;
     plan->wave_grid_m = 2;
     plan->wave_grid_n = 2;
     plan->wave_tile_m = 2;
     plan->wave_tile_n = 2;
     plan->frag_m = 16;
     plan->frag_n = 16;
-    plan->frag_k = dtype == MB_DT_FLOAT8_E4M3FN ? 128 : 32;
+    plan->frag_k = is_fp8(dtype) ? 128 : 32;
     plan->k_stages = 1;
     plan->split_k = 1;
     plan->tile_group_m = 1;
@@ -160,6 +162,10 @@ int gemm_generic_launch(int dtype, const void* A, const void* B, void* C, int64_
             break;
         case MB_DT_FLOAT8_E4M3FN:
             hipLaunchKernelGGL(gemm_generic_kernel<MB_DT_FLOAT8_E4M3FN>, grid, dim3(kGenThreads), 0,
+                               stream, A, B, C, M, N, K, alpha);
+            break;
+        case MB_DT_FLOAT8_E5M2:
+            hipLaunchKernelGGL(gemm_generic_kernel<MB_DT_FLOAT8_E5M2>, grid, dim3(kGenThreads), 0,
                                stream, A, B, C, M, N, K, alpha);
             break;
         default:

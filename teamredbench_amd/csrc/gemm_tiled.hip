@@ -1,6 +1,6 @@
 // LDS-pipelined MFMA GEMM for gfx950: C = alpha * (A * B), A (M x K) and
-// B (K x N) row-major, fp32 accumulation, output bf16 (bf16 and fp8 e4m3
-// inputs) or fp16 (fp16 inputs). Takes shapes with M % BM == 0,
+// B (K x N) row-major, fp32 accumulation, output bf16 (bf16 and fp8 e4m3 /
+// e5m2 inputs) or fp16 (fp16 inputs). Takes shapes with M % BM == 0,
 // N % BN == 0 and K a multiple of the stage depth; everything else goes to
 // the generic kernel.
 //
@@ -122,6 +122,14 @@ struct Traits<MB_DT_FLOAT8_E4M3FN> {
     // unscaled encoding of the instruction.
     __device__ static __forceinline__ f32x16 mfma(const Frag& a, const Frag& b, f32x16 c) {
         return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0);
+    }
+};
+
+// Format code 1 = bf8 e5m2 for both operands.
+template <>
+struct Traits<MB_DT_FLOAT8_E5M2> : Traits<MB_DT_FLOAT8_E4M3FN> {
+    __device__ static __forceinline__ f32x16 mfma(const Frag& a, const Frag& b, f32x16 c) {
+        return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 1, 1, 0, 0, 0, 0);
     }
 };
 
@@ -541,7 +549,7 @@ int launch_dtype(const GemmPlan& plan, const void* A, const void* B, void* C, in
 // the 32-bit range of buffer addressing).
 int gemm_tiled_plan(int dtype, int64_t M, int64_t N, int64_t K, const DeviceProps& props,
                     GemmPlan* plan) {
-    const int64_t e = dtype == MB_DT_FLOAT8_E4M3FN ? 1 : 2;
+    const int64_t e = is_fp8(dtype) ? 1 : 2;
     const int64_t stage_k = kStageK / e;
     if (K % stage_k != 0 || N % 256 != 0) return MB_ERR_SHAPE;
     if (K * N * e >= (int64_t(1) << 31) || 256 * K * e >= (int64_t(1) << 31) || M >= (int64_t(1) << 31) ||
@@ -583,7 +591,7 @@ int gemm_tiled_plan(int dtype, int64_t M, int64_t N, int64_t K, const DeviceProp
     plan->wave_tile_n = c.bn / c.wgn / 32;
     plan->frag_m = 32;
     plan->frag_n = 32;
-    plan->frag_k = dtype == MB_DT_FLOAT8_E4M3FN ? 64 : 16;
+    plan->frag_k = is_fp8(dtype) ? 64 : 16;
     plan->k_stages = c.stages;
     plan->split_k = splits;
     plan->tile_group_m = c.group_m;
@@ -602,6 +610,8 @@ int gemm_tiled_launch(int dtype, const void* A, const void* B, void* C, int64_t 
             return launch_dtype<MB_DT_FLOAT16>(plan, A, B, C, M, N, K, alpha, workspace, stream);
         case MB_DT_FLOAT8_E4M3FN:
             return launch_dtype<MB_DT_FLOAT8_E4M3FN>(plan, A, B, C, M, N, K, alpha, workspace, stream);
+        case MB_DT_FLOAT8_E5M2:
+            return launch_dtype<MB_DT_FLOAT8_E5M2>(plan, A, B, C, M, N, K, alpha, workspace, stream);
         default:
             set_error("tiled GEMM: unsupported dtype %d", dtype);
             return MB_ERR_UNSUPPORTED;

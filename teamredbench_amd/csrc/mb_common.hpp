@@ -49,6 +49,7 @@ int current_device_props(const DeviceProps** out);
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef double f64x4 __attribute__((ext_vector_type(4)));
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 typedef int i32x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
@@ -64,6 +65,7 @@ inline int dtype_size(int dtype) {
         case MB_DT_FLOAT64: return 8;
         case MB_DT_INT8: return 1;
         case MB_DT_FLOAT8_E4M3FN: return 1;
+        case MB_DT_FLOAT8_E5M2: return 1;
         default: return 0;
     }
 }
@@ -76,6 +78,7 @@ inline const char* dtype_name(int dtype) {
         case MB_DT_FLOAT64: return "float64";
         case MB_DT_INT8: return "int8";
         case MB_DT_FLOAT8_E4M3FN: return "float8_e4m3fn";
+        case MB_DT_FLOAT8_E5M2: return "float8_e5m2";
         default: return "unknown";
     }
 }

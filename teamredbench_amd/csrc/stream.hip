@@ -384,7 +384,7 @@ int stream_plan(int op, int dtype, const void* dst, const void* b, const void* c
         return MB_ERR_INVALID_ARG;
     }
     const int esize = dtype_size(dtype);
-    if (esize == 0 || dtype == MB_DT_FLOAT8_E4M3FN) {
+    if (esize == 0 || dtype == MB_DT_FLOAT8_E4M3FN || dtype == MB_DT_FLOAT8_E5M2) {
         set_error("unsupported dtype %d for stream op", dtype);
         return MB_ERR_UNSUPPORTED;
     }

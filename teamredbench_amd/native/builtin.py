@@ -18,7 +18,7 @@ register_native_kernel(
 register_native_kernel(
     name="mfu_gfx950",
     benchmark="mfu",
-    description="gfx950 MFMA GEMM (bf16/fp16/fp8 e4m3, fp32 accumulate) via the C ABI.",
+    description="gfx950 MFMA GEMM (bf16/fp16/fp8 e4m3 and e5m2 with fp32 accumulate; fp32; fp64) via the C ABI.",
     source_path=CSRC_DIR / "gemm.hip",
     abi=ABI_CAPI,
     aliases=("mfu_hipblas",),

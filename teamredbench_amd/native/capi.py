@@ -34,7 +34,7 @@ MB_ERR_DEVICE = -5
 OP_COPY, OP_SCALE, OP_TRIAD = 0, 1, 2
 OPS = {"copy": OP_COPY, "scale": OP_SCALE, "triad": OP_TRIAD}
 
-DT_FLOAT32, DT_BFLOAT16, DT_FLOAT16, DT_FLOAT64, DT_INT8, DT_FLOAT8_E4M3FN = 0, 1, 2, 3, 4, 5
+DT_FLOAT32, DT_BFLOAT16, DT_FLOAT16, DT_FLOAT64, DT_INT8, DT_FLOAT8_E4M3FN, DT_FLOAT8_E5M2 = 0, 1, 2, 3, 4, 5, 6
 DTYPES = {
     "float32": DT_FLOAT32,
     "bfloat16": DT_BFLOAT16,
@@ -42,9 +42,14 @@ DTYPES = {
     "float64": DT_FLOAT64,
     "int8": DT_INT8,
     "float8_e4m3fn": DT_FLOAT8_E4M3FN,
+    "float8_e5m2": DT_FLOAT8_E5M2,
 }
 STREAM_DTYPES = ("float32", "bfloat16", "float16", "float64", "int8")
-GEMM_DTYPES = ("bfloat16", "float16", "float8_e4m3fn")
+GEMM_DTYPES = ("bfloat16", "float16", "float8_e4m3fn", "float8_e5m2", "float32", "float64")
+FP8_DTYPES = ("float8_e4m3fn", "float8_e5m2")
+# C's element type per GEMM input type: fp8 inputs produce bf16, the others their own type.
+GEMM_OUTPUT_DTYPES = {"bfloat16": "bfloat16", "float16": "float16", "float8_e4m3fn": "bfloat16",
+                      "float8_e5m2": "bfloat16", "float32": "float32", "float64": "float64"}
 
 KIND_STREAM, KIND_GEMM = 0, 1
 

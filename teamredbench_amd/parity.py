@@ -7,7 +7,8 @@ from __future__ import annotations
 from typing import Any
 
 STREAM_ULP_BOUND = 1
-GEMM_REL_FROBENIUS_BOUND = {"bfloat16": 1e-2, "float16": 1e-2, "float8_e4m3fn": 5e-2}
+GEMM_REL_FROBENIUS_BOUND = {"bfloat16": 1e-2, "float16": 1e-2, "float8_e4m3fn": 5e-2, "float8_e5m2": 5e-2,
+                            "float32": 1e-5, "float64": 1e-12}
 
 
 def _ordered(torch: Any, x: Any) -> Any:

@@ -57,9 +57,14 @@ def seeded_uniform(torch_module: Any, numel: int, dtype_name: str, device: Any, 
     return values.to(getattr(torch, dtype_name))
 
 
+# Largest finite value of each fp8 format (the per-tensor quantisation target).
+FP8_MAX = {"float8_e4m3fn": 448.0, "float8_e5m2": 57344.0}
+
+
 def seeded_gemm_operands(torch_module: Any, m: int, n: int, k: int, dtype_name: str, device: Any, seed: int):
-    """GEMM operands on the device: normal(0, 1/sqrt(k)) for bf16/f16; for fp8
-    normal(0, 1) scaled per tensor so amax -> 448, cast to e4m3fn.
+    """GEMM operands on the device: normal(0, 1/sqrt(k)) for bf16/f16/f32/f64;
+    for fp8 normal(0, 1) scaled per tensor so amax maps to the format's
+    largest finite value (448 for e4m3fn, 57344 for e5m2) and cast.
     Returns (a, b, scale_a, scale_b)."""
     torch = torch_module
     ga = torch.Generator(device=device)
@@ -68,10 +73,13 @@ def seeded_gemm_operands(torch_module: Any, m: int, n: int, k: int, dtype_name: 
     gb.manual_seed(seed + 1)
     a = torch.randn(m, k, device=device, dtype=torch.float32, generator=ga)
     b = torch.randn(k, n, device=device, dtype=torch.float32, generator=gb)
-    if dtype_name == "float8_e4m3fn":
-        sa = float(a.abs().max()) / 448.0
-        sb = float(b.abs().max()) / 448.0
-        return (a / sa).to(torch.float8_e4m3fn), (b / sb).to(torch.float8_e4m3fn), sa, sb
+    if dtype_name in FP8_MAX:
+        fp8 = getattr(torch, dtype_name)
+        sa = float(a.abs().max()) / FP8_MAX[dtype_name]
+        sb = float(b.abs().max()) / FP8_MAX[dtype_name]
+        return (a / sa).to(fp8), (b / sb).to(fp8), sa, sb
+    if dtype_name == "float64":
+        a, b = a.double(), b.double()
     dtype = getattr(torch, dtype_name)
     std = 1.0 / math.sqrt(k)
     return (a * std).to(dtype), (b * std).to(dtype), 1.0, 1.0

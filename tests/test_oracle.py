@@ -78,6 +78,56 @@ def test_e4m3_decode_matches_torch_and_format_kats():
     assert ours[0x38] == 1.0
 
 
+def test_e5m2_decode_matches_torch_and_format_kats():
+    codes = np.arange(256, dtype=np.uint8)
+    ours = clib.decode_e5m2(codes)
+    theirs = torch.from_numpy(codes.copy()).view(torch.float8_e5m2).float().numpy()
+    nan = np.isnan(theirs)
+    assert np.array_equal(nan, np.isnan(ours))
+    assert np.array_equal(ours[~nan], theirs[~nan])
+    assert set(codes[nan].tolist()) == {0x7D, 0x7E, 0x7F, 0xFD, 0xFE, 0xFF}
+    assert ours[0x7C] == np.inf and ours[0xFC] == -np.inf
+    assert ours[0x7B] == 57344.0 and ours[0xFB] == -57344.0   # max finite
+    assert ours[0x01] == 2.0**-16                             # min subnormal
+    assert ours[0x04] == 2.0**-14                             # min normal
+    assert ours[0x3C] == 1.0 and ours[0x3D] == 1.25
+
+
+def test_e5m2_quantisation_rounds_to_nearest_even_and_saturates_to_inf():
+    # 1.125 lies halfway between 1.0 and 1.25: ties go to the even mantissa (1.0);
+    # 1.375 lies between 1.25 and 1.5: to 1.5 (even). Beyond 61440 the cast overflows.
+    x = torch.tensor([1.125, 1.375, 57344.0, 61440.0, -2.0**-17, 2.0**-17 * 3])
+    q = x.to(torch.float8_e5m2)
+    got = clib.decode_e5m2(q.view(torch.uint8).numpy())
+    assert got[0] == 1.0 and got[1] == 1.5 and got[2] == 57344.0
+    assert np.isinf(got[3])
+    assert got[4] == 0.0 and np.signbit(got[4])    # -2^-17 ties to -0
+    assert got[5] == 2.0**-15                        # 1.5 * 2^-16 ties to 2 * 2^-16
+
+
+def test_e5m2_gemm_inputs_round_trip():
+    ops = rp.gemm_inputs(64, 48, 128, "float8_e5m2", seed=0)
+    for key, scale in (("a", ops["scale_a"]), ("b", ops["scale_b"])):
+        q = ops[key]
+        assert q.dtype == torch.float8_e5m2
+        deq = clib.decode_e5m2(q.view(torch.uint8).numpy())
+        assert np.isfinite(deq).all() and np.abs(deq).max() == 57344.0
+    # the oracle product is the fp64 product of the decoded operands, scaled
+    a = clib.decode_e5m2(ops["a"].view(torch.uint8).numpy()).astype(np.float64) * ops["scale_a"]
+    b = clib.decode_e5m2(ops["b"].view(torch.uint8).numpy()).astype(np.float64) * ops["scale_b"]
+    ref = rp.gemm_reference(ops["a"], ops["b"], ops["scale_a"], ops["scale_b"]).numpy().astype(np.float64)
+    assert np.abs(ref - a @ b).max() <= 1e-5 * np.abs(a @ b).max()
+
+
+def test_float64_gemm_reference_stays_in_float64():
+    ops = rp.gemm_inputs(16, 8, 32, "float64", seed=3)
+    assert ops["a"].dtype == torch.float64
+    ref = rp.gemm_reference(ops["a"], ops["b"])
+    assert ref.dtype == torch.float64
+    exact = clib.gemm_f64(ops["a"].numpy(), ops["b"].numpy())
+    assert np.allclose(ref.numpy(), exact, rtol=1e-13, atol=1e-15)
+
+
 # ---------------------------------------------------------------- stream
 STREAM_DTYPES = ["float32", "bfloat16", "float16", "float64"]
 
