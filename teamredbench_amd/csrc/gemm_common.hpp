@@ -12,7 +12,7 @@ enum GemmVariant {
     kVariantHighp = 2,    // fp32 / fp64 inputs, any shape (gemm_highp.hip)
 };
 
-inline bool is_fp8(int dtype) { return dtype == MB_DT_FLOAT8_E4M3FN || dtype == MB_DT_FLOAT8_E5M2; }
+constexpr bool is_fp8(int dtype) { return dtype == MB_DT_FLOAT8_E4M3FN || dtype == MB_DT_FLOAT8_E5M2; }
 
 // One 16 x 16 MFMA step; operand fragments come from LDS (or registers)
 // through byte pointers. bf16/f16: 8 elements (16 bytes) per lane, K = 32.

@@ -191,7 +191,7 @@ __device__ __forceinline__ void tile_coords(int b, int nblocks, int tiles_m, int
     *tn = r / rows;
 }
 
-template <int DT, int BM, int BN, int WGM, int WGN, int STAGES>
+template <int DT, int BM, int BN, int WGM, int WGN, int STAGES, bool SCALED>
 __global__ void __launch_bounds__(64 * WGM * WGN)
 gemm_tiled_kernel(const unsigned char* __restrict__ A, const unsigned char* __restrict__ B,
                   unsigned char* __restrict__ C, int M, int N, int K, float alpha, int tiles_m,
@@ -441,34 +441,56 @@ gemm_tiled_kernel(const unsigned char* __restrict__ A, const unsigned char* __re
                                : wave == 1 ? slot_ptr(std::integral_constant<int, 1>{})
                                : wave == 2 ? slot_ptr(std::integral_constant<int, 2>{})
                                            : slot_ptr(std::integral_constant<int, 3>{});
+        // alpha is 1 except for scaled fp8: the unscaled instantiation skips
+        // the multiply, a VALU op per accumulator.
+        auto stage_tile = [&](auto scaled) {
 #pragma unroll
-        for (int i = 0; i < FM; ++i) {
-            const int r = 32 * i + (lane & 31);
+            for (int i = 0; i < FM; ++i) {
+                const int r = 32 * i + (lane & 31);
 #pragma unroll
-            for (int j = 0; j < FN; ++j) {
+                for (int j = 0; j < FN; ++j) {
 #pragma unroll
-                for (int g = 0; g < 4; ++g) {
-                    const f32x16& v = acc[i][j];
-                    const u32x2 packed = pack4<DT>(v[4 * g] * alpha, v[4 * g + 1] * alpha, v[4 * g + 2] * alpha,
-                                                   v[4 * g + 3] * alpha);
-                    const int chunk = (4 * j + g) ^ (r % ROW_CHUNKS);
-                    *reinterpret_cast<u32x2*>(stage + r * ROW_BYTES + chunk * 16 + 8 * half) = packed;
+                    for (int g = 0; g < 4; ++g) {
+                        const f32x16& v = acc[i][j];
+                        u32x2 packed;
+                        if constexpr (decltype(scaled)::value) {
+                            packed = pack4<DT>(v[4 * g] * alpha, v[4 * g + 1] * alpha, v[4 * g + 2] * alpha,
+                                               v[4 * g + 3] * alpha);
+                        } else {
+                            packed = pack4<DT>(v[4 * g], v[4 * g + 1], v[4 * g + 2], v[4 * g + 3]);
+                        }
+                        const int chunk = (4 * j + g) ^ (r % ROW_CHUNKS);
+                        *reinterpret_cast<u32x2*>(stage + r * ROW_BYTES + chunk * 16 + 8 * half) = packed;
+                    }
                 }
             }
-        }
+        };
+        stage_tile(std::integral_constant<bool, SCALED>{});
+        // Read-backs go out in batches of BATCH before their stores, so no
+        // store waits on the LDS read just before it.
         const int64_t ldc = (int64_t)N * 2;  // bytes per C row (16-bit output)
         constexpr int ROWS_PER_STORE = 64 / ROW_CHUNKS;
+        constexpr int STORES = WTM / ROWS_PER_STORE;
+        constexpr int BATCH = 8;
+        static_assert(STORES % BATCH == 0, "stores split into batches");
         const int c = lane % ROW_CHUNKS;
         const int r0 = lane / ROW_CHUNKS;
         int grow = tm * BM + wm * WTM + r0;
         unsigned char* cptr = C + (int64_t)grow * ldc + ((int64_t)tn * BN + wn * WTN) * 2 + c * 16;
 #pragma unroll
-        for (int p = 0; p < WTM / ROWS_PER_STORE; ++p) {
-            const int r = ROWS_PER_STORE * p + r0;
-            const u32x4 v = *reinterpret_cast<const u32x4*>(stage + r * ROW_BYTES + ((c ^ (r % ROW_CHUNKS)) << 4));
-            if (grow < M) *reinterpret_cast<u32x4*>(cptr) = v;
-            grow += ROWS_PER_STORE;
-            cptr += ROWS_PER_STORE * ldc;
+        for (int p0 = 0; p0 < STORES; p0 += BATCH) {
+            u32x4 rows[BATCH];
+#pragma unroll
+            for (int p = 0; p < BATCH; ++p) {
+                const int r = ROWS_PER_STORE * (p0 + p) + r0;
+                rows[p] = *reinterpret_cast<const u32x4*>(stage + r * ROW_BYTES + ((c ^ (r % ROW_CHUNKS)) << 4));
+            }
+#pragma unroll
+            for (int p = 0; p < BATCH; ++p) {
+                if (grow < M) *reinterpret_cast<u32x4*>(cptr) = rows[p];
+                grow += ROWS_PER_STORE;
+                cptr += ROWS_PER_STORE * ldc;
+            }
         }
     } else {
         float* part = ws + (int64_t)split * M * N;
@@ -519,11 +541,20 @@ int launch_cfg(const void* A, const void* B, void* C, int64_t M, int64_t N, int6
     const int tiles_m = (int)((M + c.bm - 1) / c.bm), tiles_n = (int)(N / c.bn);
     const int splits = plan.split_k;
     float* ws = splits > 1 ? static_cast<float*>(workspace) : nullptr;
-    hipLaunchKernelGGL((gemm_tiled_kernel<DT, c.bm, c.bn, c.wgm, c.wgn, c.stages>),
-                       dim3(tiles_m * tiles_n * splits), dim3(64 * c.wgm * c.wgn), 0, stream,
-                       static_cast<const unsigned char*>(A), static_cast<const unsigned char*>(B),
-                       static_cast<unsigned char*>(C), (int)M, (int)N, (int)K, alpha, tiles_m, tiles_n,
-                       c.group_m, splits, (int)(K / splits), ws);
+    const dim3 grid(tiles_m * tiles_n * splits), block(64 * c.wgm * c.wgn);
+    const auto* a = static_cast<const unsigned char*>(A);
+    const auto* b = static_cast<const unsigned char*>(B);
+    auto* cp = static_cast<unsigned char*>(C);
+    // Only fp8 carries a scale; the split-K partials are scaled by the reduction.
+    if (is_fp8(DT) && alpha != 1.0f && splits == 1) {
+        hipLaunchKernelGGL((gemm_tiled_kernel<DT, c.bm, c.bn, c.wgm, c.wgn, c.stages, is_fp8(DT)>), grid, block, 0,
+                           stream, a, b, cp, (int)M, (int)N, (int)K, alpha, tiles_m, tiles_n, c.group_m, splits,
+                           (int)(K / splits), ws);
+    } else {
+        hipLaunchKernelGGL((gemm_tiled_kernel<DT, c.bm, c.bn, c.wgm, c.wgn, c.stages, false>), grid, block, 0,
+                           stream, a, b, cp, (int)M, (int)N, (int)K, 1.0f, tiles_m, tiles_n, c.group_m, splits,
+                           (int)(K / splits), ws);
+    }
     MB_HIP_TRY(hipGetLastError());
     if (splits > 1) {
         const int64_t quads = M * N / 4;
