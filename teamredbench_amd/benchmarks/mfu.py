@@ -4,7 +4,10 @@ API and record shape follow src/teamredbench/benchmarks/mfu.py:
   params: backend (torch|native), dtypes, shapes [[m, n, k], ...] (default
           4096^3 and 8192^3), warmup (10), iterations (50), native.{...}
   extension params: seed (default 0), verify (compare against torch,
-          default true; at most `verify_max_rows` rows of C, default 4096)
+          default true; at most `verify_max_rows` rows of C, default 4096),
+          warmup_seconds (default 0: untimed warmup lasts at least this
+          long, more launches than `warmup` if need be -- the part leaves
+          its low-power clock state only after tens of ms of MFMA work)
   record: case "gemm_<m>x<n>x<k>"; raw_metrics elapsed_s / achieved_ops
           (= matmul_ops_factor * m * n * k) / peak_tops, plus gemm_bytes
           ((mk + kn) * in_bytes + mn * out_bytes) for the effective-GB/s metric.
@@ -148,8 +151,15 @@ class MfuBenchmark(Benchmark):
         ws_bytes = lib.gemm_workspace_size(dt, m, n, k)
         ws = torch.empty(ws_bytes, device=device, dtype=torch.uint8) if ws_bytes else None
         stream = torch.cuda.current_stream(device).cuda_stream
-        elapsed = lib.time_gemm(dt, a.data_ptr(), b.data_ptr(), c.data_ptr(), m, n, k, sa, sb,
-                                ws.data_ptr() if ws is not None else None, ws_bytes, warmup, iterations, stream)
+        ws_ptr = ws.data_ptr() if ws is not None else None
+        warmup_s = float(self.params.get("warmup_seconds", 0.0))
+        if warmup_s > 0:
+            est = lib.time_gemm(dt, a.data_ptr(), b.data_ptr(), c.data_ptr(), m, n, k, sa, sb, ws_ptr, ws_bytes, 0, 2,
+                                stream)
+            warmup = max(warmup, int(warmup_s / est) + 1)
+            meta["warmup_launches"] = warmup
+        elapsed = lib.time_gemm(dt, a.data_ptr(), b.data_ptr(), c.data_ptr(), m, n, k, sa, sb, ws_ptr, ws_bytes,
+                                warmup, iterations, stream)
         meta = {**meta, **lib.gemm_info(dt, m, n, k)}
         if spec.name in capi.FP8_DTYPES:
             meta["scale_a"], meta["scale_b"] = sa, sb
