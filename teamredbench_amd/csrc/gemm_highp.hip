@@ -12,7 +12,9 @@
 //
 // LDS layout per stage: A transposed to [BK][BM + pad] (the MFMA hands each
 // lane one A row at a fixed k, so consecutive lanes read consecutive
-// addresses) and B as [BK][BN + pad]. The 128-byte pad puts the lanes that
+// addresses) and B as [BK][BN + pad]. The threads that load A are laid out
+// rows first, so the transposing stores of a wave also go to 64 consecutive
+// rows of one k. The 128-byte pad puts the lanes that
 // read the next k (fp32: lanes 32-63; fp64: every other group of 16) on the
 // other half of the 64 banks, so operand reads are conflict-free. 4 waves in
 // a 2 x 2 grid own 64 x 64 of C each.
@@ -100,7 +102,7 @@ gemm_highp_kernel(const T* __restrict__ A, const T* __restrict__ B, T* __restric
 #pragma unroll
         for (int q = 0; q < PER_A; ++q) {
             const int v = tid + q * kHpThreads;
-            const int row = v / (BK / V), kv = (v % (BK / V)) * V;
+            const int row = v % kHpBM, kv = (v / kHpBM) * V;
             const int64_t gm = m0 + row, gk = k0 + kv;
             if constexpr (VEC) {
                 if (gm < M && gk < K) {
@@ -137,7 +139,7 @@ gemm_highp_kernel(const T* __restrict__ A, const T* __restrict__ B, T* __restric
 #pragma unroll
         for (int q = 0; q < PER_A; ++q) {
             const int v = tid + q * kHpThreads;
-            const int row = v / (BK / V), kv = (v % (BK / V)) * V;
+            const int row = v % kHpBM, kv = (v / kHpBM) * V;
 #pragma unroll
             for (int e = 0; e < V; ++e) sa[buf][kv + e][row] = ra[q][e];
         }
