@@ -20,6 +20,9 @@ int gemm_plan(int dtype, int64_t M, int64_t N, int64_t K, const DeviceProps& pro
         return MB_ERR_INVALID_ARG;
     }
     if (dtype == MB_DT_FLOAT32 || dtype == MB_DT_FLOAT64) return gemm_highp_plan(dtype, M, N, K, plan);
+    if (std::getenv("MB_GEMM_FORCE_GENERIC") == nullptr && std::getenv("MB_GEMM_NO_GEMV") == nullptr &&
+        gemm_gemv_plan(dtype, M, N, K, props, plan) == MB_OK)
+        return MB_OK;
     if (std::getenv("MB_GEMM_FORCE_GENERIC") == nullptr &&
         gemm_tiled_plan(dtype, M, N, K, props, plan) == MB_OK)
         return MB_OK;
@@ -37,6 +40,8 @@ int gemm_launch(int dtype, const void* A, const void* B, void* C, int64_t M, int
             return gemm_tiled_launch(dtype, A, B, C, M, N, K, alpha, workspace, plan, stream);
         case kVariantHighp:
             return gemm_highp_launch(dtype, A, B, C, M, N, K, stream);
+        case kVariantGemv:
+            return gemm_gemv_launch(dtype, A, B, C, M, N, K, workspace, plan, stream);
         default:
             set_error("GEMM plan variant %d not available", plan.variant);
             return MB_ERR_UNSUPPORTED;

@@ -10,6 +10,7 @@ enum GemmVariant {
     kVariantGeneric = 0,  // any shape, bounds-checked (gemm_generic.hip)
     kVariantTiled = 1,    // N % 256, LDS-DMA pipelined, optional split-K (gemm_tiled.hip)
     kVariantHighp = 2,    // fp32 / fp64 inputs, any shape (gemm_highp.hip)
+    kVariantGemv = 3,     // bf16 / fp16 with M <= 4: streaming FMA kernel (gemm_gemv.hip)
 };
 
 constexpr bool is_fp8(int dtype) { return dtype == MB_DT_FLOAT8_E4M3FN || dtype == MB_DT_FLOAT8_E5M2; }
@@ -76,6 +77,9 @@ int gemm_tiled_launch(int dtype, const void* A, const void* B, void* C, int64_t 
 int gemm_generic_launch(int dtype, const void* A, const void* B, void* C, int64_t M, int64_t N,
                         int64_t K, float alpha, hipStream_t stream);
 int gemm_highp_plan(int dtype, int64_t M, int64_t N, int64_t K, GemmPlan* plan);
+int gemm_gemv_plan(int dtype, int64_t M, int64_t N, int64_t K, const DeviceProps& props, GemmPlan* plan);
+int gemm_gemv_launch(int dtype, const void* A, const void* B, void* C, int64_t M, int64_t N, int64_t K,
+                     void* workspace, const GemmPlan& plan, hipStream_t stream);
 int gemm_highp_launch(int dtype, const void* A, const void* B, void* C, int64_t M, int64_t N, int64_t K,
                       hipStream_t stream);
 

@@ -90,7 +90,9 @@ def test_skinny_shapes_split_k(lib, dtype, shape):
     m, n, k = shape
     info = lib.gemm_info(capi.DTYPES[dtype], m, n, k)
     splits = info["split_k"]
-    assert info["implementation"] == "gfx950_mfma32_lds_dma" and splits >= 2
+    # M <= 4 with 16-bit inputs streams B through the small-M kernel instead
+    expect = "gfx950_gemv_stream" if m <= 4 and dtype in ("bfloat16", "float16") else "gfx950_mfma32_lds_dma"
+    assert info["implementation"] == expect and splits >= 2
     assert info["workspace_bytes"] == splits * m * n * 4
     print(f"[gemm] skinny {dtype} {shape} split {splits}", flush=True)
     _check_random(lib, dtype, m, n, k, seed=m)
@@ -101,6 +103,7 @@ def test_skinny_shapes_split_k(lib, dtype, shape):
 @pytest.mark.parametrize("splits", ["1", "2", "3"])
 def test_ragged_m_and_forced_splits(lib, dtype, m, splits, monkeypatch):
     monkeypatch.setenv("MB_GEMM_SPLITS", splits)
+    monkeypatch.setenv("MB_GEMM_NO_GEMV", "1")   # exercise the tiled kernel's splits at M = 1 too
     n, k = 512, 384
     info = lib.gemm_info(capi.DTYPES[dtype], m, n, k)
     assert info["split_k"] == int(splits)
@@ -246,3 +249,38 @@ def test_highp_kernel_info(lib, dtype):
     info = lib.gemm_info(capi.DTYPES[dtype], 1000, 1000, 1000)
     assert info["implementation"] == {"float32": "gfx950_mfma_f32_32x32x2", "float64": "gfx950_mfma_f64_16x16x4"}[dtype]
     assert info["workspace_bytes"] == 0 and info["tile_m"] == 128
+
+
+@pytest.mark.parametrize("dtype", ["bfloat16", "float16"])
+@pytest.mark.parametrize("m", [1, 2, 3, 4])
+@pytest.mark.parametrize("nk", [(4096, 4096), (8, 8), (24, 1000), (1032, 72), (8192, 8192), (65544, 64)])
+def test_small_m_stream_kernel(lib, dtype, m, nk):
+    # M <= 4 streams B with fp32 FMAs; every element within the output rounding plus an fp32
+    # accumulation bound of an fp64 brute force. 65544 x 64 keeps one K split (C written directly).
+    n, k = nk
+    info = lib.gemm_info(capi.DTYPES[dtype], m, n, k)
+    assert info["implementation"] == "gfx950_gemv_stream"
+    assert info["workspace_bytes"] == (info["split_k"] * m * n * 4 if info["split_k"] > 1 else 0)
+    print(f"[gemm] small-m {dtype} m={m} n={n} k={k} splits={info['split_k']}", flush=True)
+    ops = rp.gemm_inputs(m, n, k, dtype, seed=m * 7 + k)
+    got = _gemm(lib, dtype, ops["a"], ops["b"]).float()
+    af, bf = ops["a"].float().numpy(), ops["b"].float().numpy()
+    ref = torch.from_numpy(clib.gemm_f64(af, bf)).float()
+    out_ulp = 2.0**-8 if dtype == "bfloat16" else 2.0**-11
+    bound = ref.abs() * out_ulp + (k + 1) * 2.0**-24 * (torch.from_numpy(np.abs(af)) @ torch.from_numpy(np.abs(bf)))
+    assert torch.all((got - ref).abs() <= bound + 1e-30)
+
+
+@pytest.mark.parametrize("nk", [(8, 1), (1032, 77), (4100, 64)])
+def test_small_m_off_the_stream_kernel(lib, nk):
+    # K % 8 or N % 8 off: the MFMA kernels take the shape, still within the gate
+    n, k = nk
+    info = lib.gemm_info(capi.DT_BFLOAT16, 1, n, k)
+    assert info["implementation"] != "gfx950_gemv_stream"
+    _check_random(lib, "bfloat16", 1, n, k, seed=k)
+
+
+def test_small_m_one_split_writes_c_directly(lib):
+    m, n, k = 2, 65544, 64
+    info = lib.gemm_info(capi.DT_BFLOAT16, m, n, k)
+    assert info["split_k"] == 1 and info["workspace_bytes"] == 0
