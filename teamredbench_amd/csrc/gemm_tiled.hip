@@ -43,6 +43,7 @@
 // C whose A row panels and B column panels its L2 shares.
 #include "gemm_common.hpp"
 
+#include <cmath>
 #include <cstdlib>
 #include <utility>
 
@@ -520,7 +521,16 @@ gemm_splitk_reduce_kernel(const float* __restrict__ ws, unsigned char* __restric
     const int64_t q = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (q >= quads) return;
     f32x4 sum = *reinterpret_cast<const f32x4*>(ws + 4 * q);
-    for (int s = 1; s < splits; ++s) sum += *reinterpret_cast<const f32x4*>(ws + s * plane + 4 * q);
+    // Four splits' loads in flight at a time; the adds keep split order.
+    int s = 1;
+    for (; s + 3 < splits; s += 4) {
+        f32x4 v[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) v[u] = *reinterpret_cast<const f32x4*>(ws + (s + u) * plane + 4 * q);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) sum += v[u];
+    }
+    for (; s < splits; ++s) sum += *reinterpret_cast<const f32x4*>(ws + s * plane + 4 * q);
     *reinterpret_cast<u32x2*>(C + 8 * q) = pack4<DT>(sum[0] * alpha, sum[1] * alpha, sum[2] * alpha, sum[3] * alpha);
 }
 
@@ -595,13 +605,40 @@ int gemm_tiled_plan(int dtype, int64_t M, int64_t N, int64_t K, const DeviceProp
         if (f >= 0 && f < kNumConfigs) cfg = f;
     }
     if (cfg < 0) cfg = (tiles(0) >= cus && M % kConfigs[0].bm == 0) ? 0 : 1;
-    // K splits for problems with too few tiles to fill the GPU, as long as the
-    // fp32 partials (splits * M * N * 4 bytes) stay small next to B's bytes.
+    // K splits for problems with too few tiles to fill the GPU, chosen by a
+    // cost model whose four constants were fitted to a sweep on MI355X (bf16
+    // and fp8 e4m3; M = 16..8192, N = 1024..16384, K = 2048..16384; every
+    // power-of-two split timed): it picks the measured best split or one
+    // within 3% on 49 of 52 shapes, 12% at worst. Per split count s:
+    //   MFMA:    rounds of blocks x one block's 2*BM*BN*K/s FLOP at ~6 TFLOP/s
+    //            per CU for 16-bit inputs (twice that for fp8);
+    //   stream:  the A and B bytes at ~5 TB/s, slowed by sqrt(s * N * elem /
+    //            64 KiB) once the B row bytes the splits read at once pass
+    //            64 KiB (each split reads its own K rows; more concurrent row
+    //            positions cost DRAM page locality: 16 x 8192 x 8192 bf16 runs
+    //            26 us at 4 splits and 31 us at 16);
+    //   partials (s > 1): the fp32 partials written and read back,
+    //            2 * s * M * N * 4 bytes at ~5 TB/s, plus ~5 us for the
+    //            reduction's launch.
+    // time(s) = max(MFMA, stream) + partials; the smallest time wins.
     int splits = 1;
     if (kConfigs[cfg].bm == 128) {
-        while (tiles(cfg) * splits * 2 <= 2 * cus && K % (stage_k * splits * 2) == 0 &&
-               2 * splits * M * 4 <= K * e / 4)
-            splits *= 2;
+        const double bm = kConfigs[cfg].bm, bn = kConfigs[cfg].bn;
+        const double flops_per_cu = 6.0e12 * (e == 1 ? 2.0 : 1.0), bw = 5.0e12;
+        double best = 0.0;
+        for (int64_t s = 1; s <= 32; s *= 2) {
+            if (K % (stage_k * s) != 0) continue;
+            const double rounds = (double)((tiles(cfg) * s + cus - 1) / cus);
+            const double mfma = rounds * 2.0 * bm * bn * ((double)K / (double)s) / flops_per_cu;
+            const double rows_in_flight = (double)(s * N * e) / 65536.0;
+            const double stream = (double)((K * N + M * K) * e) / bw * std::sqrt(rows_in_flight > 1.0 ? rows_in_flight : 1.0);
+            const double partials = s > 1 ? 2.0 * (double)s * (double)M * (double)N * 4.0 / bw + 5.0e-6 : 0.0;
+            const double t = (mfma > stream ? mfma : stream) + partials;
+            if (s == 1 || t < best) {
+                best = t;
+                splits = (int)s;
+            }
+        }
     }
     const char* force_splits = std::getenv("MB_GEMM_SPLITS");  // tuning/testing override
     if (force_splits != nullptr && *force_splits != '\0') {
