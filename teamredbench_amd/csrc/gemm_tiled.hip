@@ -541,6 +541,7 @@ struct TiledConfig {
 constexpr TiledConfig kConfigs[] = {
     {256, 256, 2, 2, 5, 4},  // 0: large problems, 128 x 128 per wave, 5 x 32 KiB stages
     {128, 256, 2, 2, 6, 8},  // 1: mid-size problems, 64 x 128 per wave, 6 x 24 KiB stages
+    {128, 128, 4, 1, 6, 4},  // 2: 16-bit only, few tiles: 32 x 128 per wave, 6 x 16 KiB stages
 };
 constexpr int kNumConfigs = sizeof(kConfigs) / sizeof(kConfigs[0]);
 
@@ -580,6 +581,11 @@ template <int DT>
 int launch_dtype(const GemmPlan& plan, const void* A, const void* B, void* C, int64_t M, int64_t N, int64_t K,
                  float alpha, void* workspace, hipStream_t stream) {
     if (plan.config == 0) return launch_cfg<DT, 0>(A, B, C, M, N, K, alpha, plan, workspace, stream);
+    // 128-column tiles have 256-byte B rows for 16-bit inputs only (the fp8
+    // B swizzle assumes 256-byte rows of 256 columns).
+    if constexpr (!is_fp8(DT)) {
+        if (plan.config == 2) return launch_cfg<DT, 2>(A, B, C, M, N, K, alpha, plan, workspace, stream);
+    }
     return launch_cfg<DT, 1>(A, B, C, M, N, K, alpha, plan, workspace, stream);
 }
 
@@ -602,8 +608,9 @@ int gemm_tiled_plan(int dtype, int64_t M, int64_t N, int64_t K, const DeviceProp
     const char* force = std::getenv("MB_GEMM_TILED_CONFIG");  // tuning/testing override
     if (force != nullptr && *force != '\0') {
         const int f = std::atoi(force);
-        if (f >= 0 && f < kNumConfigs) cfg = f;
+        if (f >= 0 && f < kNumConfigs && !(f == 2 && e == 1)) cfg = f;
     }
+    const bool forced = cfg >= 0;
     if (cfg < 0) cfg = (tiles(0) >= cus && M % kConfigs[0].bm == 0) ? 0 : 1;
     // K splits for problems with too few tiles to fill the GPU, chosen by a
     // cost model whose four constants were fitted to a sweep on MI355X (bf16
@@ -640,6 +647,10 @@ int gemm_tiled_plan(int dtype, int64_t M, int64_t N, int64_t K, const DeviceProp
             }
         }
     }
+    // Several tile rows, no split and at most half the CUs busy (2048^3 makes
+    // 128 tiles of 128 x 256): 16-bit inputs take 128 x 128 tiles instead,
+    // twice the blocks for the same B panel traffic per tile row.
+    if (!forced && cfg == 1 && splits == 1 && e == 2 && M > kConfigs[1].bm && tiles(1) * 2 <= cus) cfg = 2;
     const char* force_splits = std::getenv("MB_GEMM_SPLITS");  // tuning/testing override
     if (force_splits != nullptr && *force_splits != '\0') {
         const int f = std::atoi(force_splits);

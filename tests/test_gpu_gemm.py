@@ -68,18 +68,34 @@ def test_gemm_random_matches_fp32_matmul(lib, dtype, shape):
 
 
 @pytest.mark.parametrize("dtype", LOWP)
-@pytest.mark.parametrize("config", ["0", "1"])
+@pytest.mark.parametrize("config", ["0", "1", "2"])
 @pytest.mark.parametrize("shape", [(256, 256, 128), (256, 512, 64), (256, 512, 1024), (512, 256, 4096), (768, 1280, 384)])
 def test_tiled_configurations(lib, dtype, config, shape, monkeypatch):
     # Every tiled configuration on shapes it divides, selected through the
-    # configuration override; the plan names the kernel that ran.
+    # configuration override; the plan names the kernel that ran. The
+    # 128 x 128 configuration takes 16-bit inputs only (fp8 keeps its default).
     monkeypatch.setenv("MB_GEMM_TILED_CONFIG", config)
     m, n, k = shape
     info = lib.gemm_info(capi.DTYPES[dtype], m, n, k)
     assert info["implementation"] == "gfx950_mfma32_lds_dma"
-    assert info["tile_m"] == (256 if config == "0" else 128)
+    if config == "2" and dtype.startswith("float8"):
+        assert info["tile_n"] == 256
+    else:
+        assert (info["tile_m"], info["tile_n"]) == {"0": (256, 256), "1": (128, 256), "2": (128, 128)}[config]
     print(f"[gemm] tiled cfg {config} {dtype} {shape}", flush=True)
     _check_random(lib, dtype, m, n, k, seed=k)
+
+
+@pytest.mark.parametrize("dtype", ["bfloat16", "float16"])
+@pytest.mark.parametrize("shape", [(2048, 2048, 2048), (1024, 1024, 1024), (640, 1536, 768)])
+def test_few_tiles_take_128x128_tiles(lib, dtype, shape):
+    # Several tile rows that would leave half the CUs idle on 128 x 256 tiles
+    # run 128 x 128 tiles, unsplit (the default plan, not an override).
+    m, n, k = shape
+    info = lib.gemm_info(capi.DTYPES[dtype], m, n, k)
+    assert (info["tile_m"], info["tile_n"], info["split_k"]) == (128, 128, 1)
+    print(f"[gemm] 128x128 default {dtype} {shape}", flush=True)
+    _check_random(lib, dtype, m, n, k, seed=n)
 
 
 @pytest.mark.parametrize("dtype", LOWP)
