@@ -19,7 +19,7 @@ int gemm_plan(int dtype, int64_t M, int64_t N, int64_t K, const DeviceProps& pro
                   (long long)K);
         return MB_ERR_INVALID_ARG;
     }
-    if (dtype == MB_DT_FLOAT32 || dtype == MB_DT_FLOAT64) return gemm_highp_plan(dtype, M, N, K, plan);
+    if (dtype == MB_DT_FLOAT32 || dtype == MB_DT_FLOAT64) return gemm_highp_plan(dtype, M, N, K, props, plan);
     if (std::getenv("MB_GEMM_FORCE_GENERIC") == nullptr && std::getenv("MB_GEMM_NO_GEMV") == nullptr &&
         gemm_gemv_plan(dtype, M, N, K, props, plan) == MB_OK)
         return MB_OK;
@@ -39,7 +39,7 @@ int gemm_launch(int dtype, const void* A, const void* B, void* C, int64_t M, int
         case kVariantTiled:
             return gemm_tiled_launch(dtype, A, B, C, M, N, K, alpha, workspace, plan, stream);
         case kVariantHighp:
-            return gemm_highp_launch(dtype, A, B, C, M, N, K, stream);
+            return gemm_highp_launch(dtype, A, B, C, M, N, K, plan, stream);
         case kVariantGemv:
             return gemm_gemv_launch(dtype, A, B, C, M, N, K, workspace, plan, stream);
         default:

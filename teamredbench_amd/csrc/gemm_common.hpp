@@ -76,11 +76,11 @@ int gemm_tiled_launch(int dtype, const void* A, const void* B, void* C, int64_t 
                       int64_t K, float alpha, void* workspace, const GemmPlan& plan, hipStream_t stream);
 int gemm_generic_launch(int dtype, const void* A, const void* B, void* C, int64_t M, int64_t N,
                         int64_t K, float alpha, hipStream_t stream);
-int gemm_highp_plan(int dtype, int64_t M, int64_t N, int64_t K, GemmPlan* plan);
+int gemm_highp_plan(int dtype, int64_t M, int64_t N, int64_t K, const DeviceProps& props, GemmPlan* plan);
 int gemm_gemv_plan(int dtype, int64_t M, int64_t N, int64_t K, const DeviceProps& props, GemmPlan* plan);
 int gemm_gemv_launch(int dtype, const void* A, const void* B, void* C, int64_t M, int64_t N, int64_t K,
                      void* workspace, const GemmPlan& plan, hipStream_t stream);
 int gemm_highp_launch(int dtype, const void* A, const void* B, void* C, int64_t M, int64_t N, int64_t K,
-                      hipStream_t stream);
+                      const GemmPlan& plan, hipStream_t stream);
 
 }  // namespace mb

@@ -23,7 +23,9 @@
 // alignment (K and N multiples of 16 / elem bytes); otherwise element-wise.
 // Either way elements outside the matrices read as zero and stores outside C
 // are skipped, so ragged edges need no separate kernel.
-#include "gemm_common.hpp"
+#include "gemm_pipeline.hpp"
+
+#include <cstdlib>
 
 namespace mb {
 namespace {
@@ -199,6 +201,168 @@ gemm_highp_kernel(const T* __restrict__ A, const T* __restrict__ B, T* __restric
     }
 }
 
+// ---- fp32 on an LDS-DMA ring (256 x 256 tiles) -----------------------------
+//
+// The register-staged kernel above tops out near 80% of the fp32 peak: its
+// load, LDS store and barrier phases leave the matrix pipe idle between MFMA
+// groups. This one follows the 16-bit pipelined kernel instead: A and B go
+// global -> LDS with buffer_load ... lds into a ring of 4 slots (one barrier
+// per stage, loads of stage kt + 3 issued into the slot stage kt - 1 just
+// vacated), and each wave owns 128 x 128 of C as 4 x 4 fragments of
+// v_mfma_f32_32x32x2_f32, so a stage is 128 MFMAs (8192 cycles) against one
+// barrier.
+//
+// K order inside a stage. The MFMA sums two K values, one from each lane
+// half; here lane half h supplies K 8h + t at step t (t = 0..7), which is any
+// fixed permutation of the stage's 16 K values and leaves the sum the same.
+// So a lane's A operands for the whole stage are 8 consecutive floats of one
+// row -- two ds_read_b128 per fragment from the [256 rows][64 B] A slot (the
+// 16-bit kernel's layout and swizzle) -- and its B operand at step t is one
+// float of row 8h + t, read with ds_read_b32. B keeps its HBM layout ([16
+// rows][1024 B]); rows 8..15 have their 16-byte chunks XOR 8, so the two lane
+// halves, which read rows 8 apart (8 KiB, the same banks), land 128 bytes
+// apart and the read is conflict-free.
+//
+// The MFMA takes the B operand first, so a lane's 16 accumulators of a
+// fragment hold one C row, 4 runs of 4 consecutive columns; the epilogue
+// stores them as 16-byte pieces straight from registers (a tile computes for
+// milliseconds; its 256 KiB of C do not need LDS staging).
+constexpr int kF32Tile = 256, kF32Stages = 4, kF32StageK = 16;
+constexpr int kF32ABytes = kF32Tile * 64;                  // [256 rows][64 B]
+constexpr int kF32BRow = kF32Tile * 4;                     // 1024 B
+constexpr int kF32BBytes = kF32StageK * kF32BRow;          // [16 rows][1024 B]
+constexpr int kF32Slot = kF32ABytes + kF32BBytes;          // 32 KiB
+constexpr int kF32AInstr = kF32ABytes / 1024 / 4;          // DMA instructions per wave per stage
+constexpr int kF32BInstr = kF32BBytes / 1024 / 4;
+constexpr int kF32Loads = kF32AInstr + kF32BInstr;
+constexpr int kF32GroupM = 4;
+
+__device__ __forceinline__ int swz_b32(int row) { return ((row >> 3) & 1) << 3; }
+
+__global__ void __launch_bounds__(256)
+gemm_f32_dma_kernel(const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ C, int M, int N,
+                    int K, int tiles_m, int tiles_n) {
+    __shared__ __attribute__((aligned(1024))) unsigned char ring[kF32Stages][kF32Slot];
+    const int tid = threadIdx.x, lane = tid & 63, half = lane >> 5;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave >> 1, wn = wave & 1;
+    int tm, tn;
+    tile_coords((int)blockIdx.x, tiles_m * tiles_n, tiles_m, tiles_n, kF32GroupM, &tm, &tn);
+    const int lda = K * 4, ldb = N * 4;
+    const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(A) + (int64_t)tm * kF32Tile * K, (short)0, kF32Tile * lda, kBufferFlags);
+    const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(B) + (int64_t)tn * kF32Tile, (short)0, K * ldb, kBufferFlags);
+    int a_voff[kF32AInstr], b_voff[kF32BInstr];
+#pragma unroll
+    for (int q = 0; q < kF32AInstr; ++q) {
+        const int lin = (wave * kF32AInstr + q) * 1024 + lane * 16;
+        const int row = lin / 64, pchunk = (lin % 64) >> 4;
+        a_voff[q] = row * lda + ((pchunk ^ swz_a(row)) << 4);
+    }
+#pragma unroll
+    for (int q = 0; q < kF32BInstr; ++q) {
+        const int lin = (wave * kF32BInstr + q) * 1024 + lane * 16;
+        const int row = lin / kF32BRow, pchunk = (lin % kF32BRow) >> 4;
+        b_voff[q] = row * ldb + ((pchunk ^ swz_b32(row)) << 4);
+    }
+    auto issue = [&](int kt, int slot) {
+        const unsigned base = (unsigned)(uintptr_t)(MB_LDS unsigned char*)ring[slot];
+#pragma unroll
+        for (int q = 0; q < kF32AInstr; ++q)
+            lds_dma16(ra, base + (wave * kF32AInstr + q) * 1024, a_voff[q], kt * 64);
+#pragma unroll
+        for (int q = 0; q < kF32BInstr; ++q)
+            lds_dma16(rb, base + kF32ABytes + (wave * kF32BInstr + q) * 1024, b_voff[q], kt * kF32StageK * ldb);
+    };
+
+    f32x16 acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+    const int ksteps = K / kF32StageK, last = ksteps - 1;
+#pragma unroll
+    for (int st = 0; st < kF32Stages - 1; ++st) issue(min(st, last), st);
+    const int a_row = wm * 128 + (lane & 31);
+    const int b_col = wn * 128 + (lane & 31);
+    for (int kt = 0; kt < ksteps; ++kt) {
+        // Stage kt has landed for every wave, and every wave has finished
+        // reading the slot of stage kt - 1, which takes stage kt + 3's loads
+        // (past the last stage they repeat it: in bounds, never read).
+        wait_vmcnt_and_barrier<kF32Loads * (kF32Stages - 2)>();
+        issue(min(kt + kF32Stages - 1, last), (kt + kF32Stages - 1) % kF32Stages);
+        const unsigned char* slot = ring[kt % kF32Stages];
+        const unsigned char* sb = slot + kF32ABytes;
+        float a[4][8];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int row = a_row + 32 * i;
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                // Read as whole float vectors: __builtin_bit_cast of a single
+                // ext_vector element (bit_cast(float, v[w]) on a u32x4) is
+                // miscompiled by this clang -- it reuses element 0 and drops
+                // the other loads.
+                const f32x4 v = *reinterpret_cast<const f32x4*>(slot + row * 64 + (((2 * half + e) ^ swz_a(row)) << 4));
+#pragma unroll
+                for (int w = 0; w < 4; ++w) a[i][4 * e + w] = v[w];
+            }
+        }
+        float b[2][4];
+        auto read_b = [&](int t, int set) {
+            const int row = 8 * half + t;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int col = b_col + 32 * j;
+                b[set][j] = *reinterpret_cast<const float*>(sb + row * kF32BRow + (((col >> 2) ^ swz_b32(row)) << 4) +
+                                                            4 * (col & 3));
+            }
+        };
+        read_b(0, 0);
+#pragma unroll
+        for (int t = 0; t < kF32StageK / 2; ++t) {
+            if (t + 1 < kF32StageK / 2) read_b(t + 1, (t + 1) & 1);
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(b[t & 1][j], a[i][t], acc[i][j], 0, 0, 0);
+        }
+    }
+    wait_vmcnt_and_barrier<0>();
+
+    // Accumulator register 4g + q of lane l holds C[row 32i + l % 32]
+    // [col 32j + 8g + 4 * (l / 32) + q] of the wave's tile.
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        float* crow = C + (int64_t)(tm * kF32Tile + wm * 128 + 32 * i + (lane & 31)) * N + tn * kF32Tile + wn * 128 +
+                      4 * half;
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const f32x4 v = {acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]};
+                *reinterpret_cast<f32x4*>(crow + 32 * j + 8 * g) = v;
+            }
+    }
+}
+
+// Shapes the DMA kernel takes: whole 256 x 256 tiles, K in whole stages,
+// buffer offsets (B's K x N bytes, a 256-row A panel) within 31 bits, and at
+// least one tile per CU -- with fewer (2048^3 makes 64), the staged kernel's
+// 128 x 128 tiles keep more of the GPU busy (2048^3: 98 against 35 TFLOP/s).
+bool f32_dma_fits(int64_t M, int64_t N, int64_t K, int cus) {
+    if (std::getenv("MB_GEMM_HIGHP_REGISTER") != nullptr) return false;  // testing override: staged kernel
+    const int64_t tiles = (M / kF32Tile) * (N / kF32Tile);
+    return M % kF32Tile == 0 && N % kF32Tile == 0 && K % kF32StageK == 0 && K * N * 4 < (int64_t(1) << 31) &&
+           kF32Tile * K * 4 < (int64_t(1) << 31) && tiles <= INT32_MAX && tiles >= cus;
+}
+
 template <typename T>
 int launch_typed(const void* A, const void* B, void* C, int64_t M, int64_t N, int64_t K, hipStream_t stream) {
     constexpr int V = 16 / (int)sizeof(T);
@@ -217,9 +381,26 @@ int launch_typed(const void* A, const void* B, void* C, int64_t M, int64_t N, in
 
 }  // namespace
 
-int gemm_highp_plan(int dtype, int64_t M, int64_t N, int64_t K, GemmPlan* plan) {
-    (void)K;
+int gemm_highp_plan(int dtype, int64_t M, int64_t N, int64_t K, const DeviceProps& props, GemmPlan* plan) {
     const bool f64 = dtype == MB_DT_FLOAT64;
+    if (!f64 && f32_dma_fits(M, N, K, props.cu_count > 0 ? props.cu_count : 256)) {
+        plan->implementation = "gfx950_mfma_f32_32x32x2_lds_dma";
+        plan->threads = 256;
+        plan->grid = (int)((M / kF32Tile) * (N / kF32Tile));
+        plan->tile_m = plan->tile_n = kF32Tile;
+        plan->tile_k = kF32StageK;
+        plan->wave_grid_m = plan->wave_grid_n = 2;
+        plan->frag_m = plan->frag_n = 32;
+        plan->frag_k = 2;
+        plan->wave_tile_m = plan->wave_tile_n = 4;
+        plan->k_stages = kF32Stages;
+        plan->split_k = 1;
+        plan->tile_group_m = kF32GroupM;
+        plan->workspace = 0;
+        plan->variant = kVariantHighp;
+        plan->config = 1;
+        return MB_OK;
+    }
     const int64_t gx = (N + kHpBN - 1) / kHpBN, gy = (M + kHpBM - 1) / kHpBM;
     if (gy > 65535 || gx > INT32_MAX) {
         set_error("fp32/fp64 GEMM: M=%lld N=%lld too large", (long long)M, (long long)N);
@@ -245,9 +426,18 @@ int gemm_highp_plan(int dtype, int64_t M, int64_t N, int64_t K, GemmPlan* plan) 
 }
 
 int gemm_highp_launch(int dtype, const void* A, const void* B, void* C, int64_t M, int64_t N, int64_t K,
-                      hipStream_t stream) {
+                      const GemmPlan& plan, hipStream_t stream) {
     switch (dtype) {
-        case MB_DT_FLOAT32: return launch_typed<float>(A, B, C, M, N, K, stream);
+        case MB_DT_FLOAT32:
+            if (plan.config == 1) {
+                const int tiles_m = (int)(M / kF32Tile), tiles_n = (int)(N / kF32Tile);
+                hipLaunchKernelGGL(gemm_f32_dma_kernel, dim3(tiles_m * tiles_n), dim3(256), 0, stream,
+                                   static_cast<const float*>(A), static_cast<const float*>(B), static_cast<float*>(C),
+                                   (int)M, (int)N, (int)K, tiles_m, tiles_n);
+                MB_HIP_TRY(hipGetLastError());
+                return MB_OK;
+            }
+            return launch_typed<float>(A, B, C, M, N, K, stream);
         case MB_DT_FLOAT64: return launch_typed<double>(A, B, C, M, N, K, stream);
         default:
             set_error("fp32/fp64 GEMM: unsupported dtype %d", dtype);

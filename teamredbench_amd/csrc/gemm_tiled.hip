@@ -41,7 +41,7 @@
 // XCD b % 8); each XCD gets a contiguous range of tiles in an order grouped
 // by `group_m` tile rows, i.e. a compact group_m x (range / group_m) patch of
 // C whose A row panels and B column panels its L2 shares.
-#include "gemm_common.hpp"
+#include "gemm_pipeline.hpp"
 
 #include <cmath>
 #include <cstdlib>
@@ -50,43 +50,10 @@
 namespace mb {
 namespace {
 
-#define MB_LDS __attribute__((address_space(3)))
-
 constexpr int kStageK = 64;                  // bytes of K per row per stage
-constexpr int kBufferFlags = 0x00020000;     // raw buffer resource word 3 on gfx9
 
-__device__ __forceinline__ int swz_a(int r) { return ((r >> 1) & 3) ^ ((r >> 3) & 1); }
 __device__ __forceinline__ int swz_b16(int k) { return ((k << 2) ^ (k << 1)) & 15; }
 __device__ __forceinline__ int swz_b8(int k) { return (2 * k) ^ (k >> 2); }
-
-// Wait until at most N vector-memory operations of this wave are pending and
-// its LDS operations have drained, then join the workgroup barrier. The empty
-// asm with a memory clobber keeps the compiler from moving LDS accesses
-// across the barrier (the barrier builtin alone does not order memory).
-template <int N>
-__device__ __forceinline__ void wait_vmcnt_and_barrier() {
-    static_assert(N >= 0 && N < 64, "vmcnt is a 6-bit counter");
-    // gfx9 s_waitcnt encoding: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt[5:4] at [15:14]
-    asm volatile("" ::: "memory");
-    __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0x0 << 8));
-    __builtin_amdgcn_s_barrier();
-    asm volatile("" ::: "memory");
-}
-
-// One LDS-DMA load: every lane fetches 16 bytes at rsrc + voff + soff and the
-// wave writes them to LDS bytes [lds_addr, lds_addr + 1024) in lane order.
-// Issued as inline asm so the compiler's wait insertion, which cannot tell
-// which ring slot the write lands in, does not put a full vmcnt drain in
-// front of every later LDS read; the callers order these loads themselves.
-#pragma clang diagnostic push
-#pragma clang diagnostic ignored "-Winline-asm"
-__device__ __forceinline__ void lds_dma16(__amdgpu_buffer_rsrc_t rsrc, unsigned lds_addr, int voff, int soff) {
-    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
-                 :
-                 : "s"(lds_addr), "v"(voff), "s"(rsrc), "s"(soff)
-                 : "memory", "m0");
-}
-#pragma clang diagnostic pop
 
 typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x4_t __attribute__((__vector_size__(4 * sizeof(__bf16))));
@@ -176,20 +143,6 @@ __device__ __forceinline__ u32x2 pack4(float a, float b, float c, float d) {
         bf16x4 h = {(__bf16)a, (__bf16)b, (__bf16)c, (__bf16)d};
         return __builtin_bit_cast(u32x2, h);
     }
-}
-
-// Tile index -> (tile row, tile column), XCD-contiguous and grouped by rows.
-__device__ __forceinline__ void tile_coords(int b, int nblocks, int tiles_m, int tiles_n, int group_m,
-                                            int* tm, int* tn) {
-    int t = b;
-    if ((nblocks & 7) == 0) t = (b & 7) * (nblocks >> 3) + (b >> 3);
-    const int per_group = group_m * tiles_n;
-    const int g = t / per_group;
-    const int first_m = g * group_m;
-    const int rows = min(tiles_m - first_m, group_m);
-    const int r = t - g * per_group;
-    *tm = first_m + r % rows;
-    *tn = r / rows;
 }
 
 template <int DT, int BM, int BN, int WGM, int WGN, int STAGES, bool SCALED>

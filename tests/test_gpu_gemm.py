@@ -278,6 +278,47 @@ def test_highp_kernel_info(lib, dtype):
     assert info["workspace_bytes"] == 0 and info["tile_m"] == 128
 
 
+@pytest.mark.parametrize("shape, dma", [((4096, 4096, 64), True), ((8192, 2048, 96), True), ((4352, 4096, 16), True),
+                                        ((2048, 2048, 2048), False), ((4096, 4096, 40), False), ((4096, 4000, 64), False)])
+def test_f32_lds_dma_kernel_selection(lib, shape, dma):
+    # fp32 takes the LDS-DMA kernel for whole 256 x 256 tiles, K in steps of 16 and at least one tile
+    # per CU (2048^3 makes 64 and stays on the staged kernel's 128 x 128 tiles).
+    info = lib.gemm_info(capi.DT_FLOAT32, *shape)
+    assert (info["implementation"] == "gfx950_mfma_f32_32x32x2_lds_dma") == dma
+    assert info["tile_m"] == (256 if dma else 128) and info["workspace_bytes"] == 0
+
+
+@pytest.mark.parametrize("shape", [(4096, 4096, 64), (8192, 2048, 96)])
+def test_f32_lds_dma_against_float64_brute_force(lib, shape, monkeypatch):
+    # The LDS-DMA kernel sums each stage's 16 K values in a permuted order (lane half h takes K 8h + t
+    # at step t); every element must still sit within the fp32 accumulation bound of an fp64
+    # brute force, and the staged kernel (forced) must agree with it to the same bound.
+    m, n, k = shape
+    assert lib.gemm_info(capi.DT_FLOAT32, m, n, k)["implementation"] == "gfx950_mfma_f32_32x32x2_lds_dma"
+    print(f"[gemm] f32 lds-dma {shape}", flush=True)
+    ops = rp.gemm_inputs(m, n, k, "float32", seed=5)
+    got = _gemm(lib, "float32", ops["a"], ops["b"]).double()
+    a64, b64 = ops["a"].double().numpy(), ops["b"].double().numpy()
+    ref = torch.from_numpy(clib.gemm_f64(a64, b64))
+    mag = torch.from_numpy(np.abs(a64)) @ torch.from_numpy(np.abs(b64))
+    bound = ref.abs() * UNIT["float32"] + (k + 1) * UNIT["float32"] * mag
+    assert torch.all((got - ref).abs() <= bound)
+    monkeypatch.setenv("MB_GEMM_HIGHP_REGISTER", "1")
+    assert lib.gemm_info(capi.DT_FLOAT32, m, n, k)["implementation"] == "gfx950_mfma_f32_32x32x2"
+    staged = _gemm(lib, "float32", ops["a"], ops["b"]).double()
+    assert torch.all((staged - ref).abs() <= bound)
+
+
+def test_f32_lds_dma_constant_fill_is_exact(lib):
+    # The reference executable's constant fill: A = B = 0.03125 gives C = K / 1024 exactly.
+    m, n, k = 4096, 4096, 1024
+    a = torch.full((m, k), 0.03125)
+    b = torch.full((k, n), 0.03125)
+    assert lib.gemm_info(capi.DT_FLOAT32, m, n, k)["implementation"] == "gfx950_mfma_f32_32x32x2_lds_dma"
+    got = _gemm(lib, "float32", a, b)
+    assert torch.all(got == k / 1024)
+
+
 @pytest.mark.parametrize("dtype", ["bfloat16", "float16"])
 @pytest.mark.parametrize("m", [1, 2, 3, 4])
 @pytest.mark.parametrize("nk", [(4096, 4096), (8, 8), (24, 1000), (1032, 72), (8192, 8192), (65544, 64)])
