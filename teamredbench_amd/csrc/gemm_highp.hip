@@ -352,6 +352,132 @@ gemm_f32_dma_kernel(const float* __restrict__ A, const float* __restrict__ B, fl
     }
 }
 
+// ---- fp64 on the same LDS-DMA ring (256 x 128 tiles) -----------------------
+//
+// v_mfma_f64_16x16x4_f64 sums four K values, one from each 16-lane group g;
+// here group g supplies K 2g + t at step t (t = 0, 1) of a stage's 8, so a
+// lane's A operands for the stage are 2 consecutive doubles of one row -- one
+// ds_read_b128 per fragment from the [256 rows][64 B] A slot -- and its B
+// operand at step t is one double of row 2g + t (ds_read_b64). B keeps its HBM
+// layout, [8 rows][128 doubles = 1024 B]; rows with bit 1 set have their
+// 16-byte chunks XOR 8, so groups 0 and 1 (and 2 and 3), which read rows 2
+// apart (the same banks), land 128 bytes apart. Waves own 128 x 64 of C as
+// 8 x 4 fragments (256 accumulator registers); A is the MFMA's first operand,
+// so accumulator r of lane l is C row 4r + l / 16, column l % 16, and a store
+// instruction writes 4 rows x 128 bytes straight from registers.
+constexpr int kF64BM = 256, kF64BN = 128, kF64Stages = 4, kF64StageK = 8;
+constexpr int kF64ABytes = kF64BM * 64;                    // [256 rows][64 B]
+constexpr int kF64BRow = kF64BN * 8;                       // 1024 B
+constexpr int kF64BBytes = kF64StageK * kF64BRow;          // [8 rows][1024 B]
+constexpr int kF64Slot = kF64ABytes + kF64BBytes;          // 24 KiB
+constexpr int kF64AInstr = kF64ABytes / 1024 / 4;
+constexpr int kF64BInstr = kF64BBytes / 1024 / 4;
+constexpr int kF64Loads = kF64AInstr + kF64BInstr;
+
+__device__ __forceinline__ int swz_b64(int row) { return ((row >> 1) & 1) << 3; }
+
+__global__ void __launch_bounds__(256)
+gemm_f64_dma_kernel(const double* __restrict__ A, const double* __restrict__ B, double* __restrict__ C, int M,
+                    int N, int K, int tiles_m, int tiles_n) {
+    __shared__ __attribute__((aligned(1024))) unsigned char ring[kF64Stages][kF64Slot];
+    const int tid = threadIdx.x, lane = tid & 63, grp = lane >> 4;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave >> 1, wn = wave & 1;
+    int tm, tn;
+    tile_coords((int)blockIdx.x, tiles_m * tiles_n, tiles_m, tiles_n, kF32GroupM, &tm, &tn);
+    const int lda = K * 8, ldb = N * 8;
+    const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<double*>(A) + (int64_t)tm * kF64BM * K, (short)0, kF64BM * lda, kBufferFlags);
+    const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<double*>(B) + (int64_t)tn * kF64BN, (short)0, K * ldb, kBufferFlags);
+    int a_voff[kF64AInstr], b_voff[kF64BInstr];
+#pragma unroll
+    for (int q = 0; q < kF64AInstr; ++q) {
+        const int lin = (wave * kF64AInstr + q) * 1024 + lane * 16;
+        const int row = lin / 64, pchunk = (lin % 64) >> 4;
+        a_voff[q] = row * lda + ((pchunk ^ swz_a(row)) << 4);
+    }
+#pragma unroll
+    for (int q = 0; q < kF64BInstr; ++q) {
+        const int lin = (wave * kF64BInstr + q) * 1024 + lane * 16;
+        const int row = lin / kF64BRow, pchunk = (lin % kF64BRow) >> 4;
+        b_voff[q] = row * ldb + ((pchunk ^ swz_b64(row)) << 4);
+    }
+    auto issue = [&](int kt, int slot) {
+        const unsigned base = (unsigned)(uintptr_t)(MB_LDS unsigned char*)ring[slot];
+#pragma unroll
+        for (int q = 0; q < kF64AInstr; ++q)
+            lds_dma16(ra, base + (wave * kF64AInstr + q) * 1024, a_voff[q], kt * 64);
+#pragma unroll
+        for (int q = 0; q < kF64BInstr; ++q)
+            lds_dma16(rb, base + kF64ABytes + (wave * kF64BInstr + q) * 1024, b_voff[q], kt * kF64StageK * ldb);
+    };
+
+    f64x4 acc[8][4];
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) acc[i][j][r] = 0.0;
+
+    const int ksteps = K / kF64StageK, last = ksteps - 1;
+#pragma unroll
+    for (int st = 0; st < kF64Stages - 1; ++st) issue(min(st, last), st);
+    const int a_row = wm * 128 + (lane & 15);
+    const int b_col = wn * 64 + (lane & 15);
+    for (int kt = 0; kt < ksteps; ++kt) {
+        wait_vmcnt_and_barrier<kF64Loads * (kF64Stages - 2)>();
+        issue(min(kt + kF64Stages - 1, last), (kt + kF64Stages - 1) % kF64Stages);
+        const unsigned char* slot = ring[kt % kF64Stages];
+        const unsigned char* sb = slot + kF64ABytes;
+        double a[8][2];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int row = a_row + 16 * i;
+            const f64x2 v = *reinterpret_cast<const f64x2*>(slot + row * 64 + ((grp ^ swz_a(row)) << 4));
+            a[i][0] = v[0];
+            a[i][1] = v[1];
+        }
+        double b[2][4];
+#pragma unroll
+        for (int t = 0; t < kF64StageK / 4; ++t) {
+            const int row = 2 * grp + t;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int col = b_col + 16 * j;
+                b[t][j] = *reinterpret_cast<const double*>(sb + row * kF64BRow + (((col >> 1) ^ swz_b64(row)) << 4) +
+                                                           8 * (col & 1));
+            }
+        }
+#pragma unroll
+        for (int t = 0; t < kF64StageK / 4; ++t)
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f64_16x16x4f64(a[i][t], b[t][j], acc[i][j], 0, 0, 0);
+    }
+    wait_vmcnt_and_barrier<0>();
+
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            double* crow = C + (int64_t)(tm * kF64BM + wm * 128 + 16 * i + 4 * r + grp) * N + tn * kF64BN + wn * 64 +
+                           (lane & 15);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) crow[16 * j] = acc[i][j][r];
+        }
+}
+
+bool f64_dma_fits(int64_t M, int64_t N, int64_t K, int cus) {
+    if (std::getenv("MB_GEMM_HIGHP_REGISTER") != nullptr) return false;  // testing override: staged kernel
+    const int64_t tiles = (M / kF64BM) * (N / kF64BN);
+    return M % kF64BM == 0 && N % kF64BN == 0 && K % kF64StageK == 0 && K * N * 8 < (int64_t(1) << 31) &&
+           kF64BM * K * 8 < (int64_t(1) << 31) && tiles <= INT32_MAX && tiles >= cus;
+}
+
 // Shapes the DMA kernel takes: whole 256 x 256 tiles, K in whole stages,
 // buffer offsets (B's K x N bytes, a 256-row A panel) within 31 bits, and at
 // least one tile per CU -- with fewer (2048^3 makes 64), the staged kernel's
@@ -383,7 +509,28 @@ int launch_typed(const void* A, const void* B, void* C, int64_t M, int64_t N, in
 
 int gemm_highp_plan(int dtype, int64_t M, int64_t N, int64_t K, const DeviceProps& props, GemmPlan* plan) {
     const bool f64 = dtype == MB_DT_FLOAT64;
-    if (!f64 && f32_dma_fits(M, N, K, props.cu_count > 0 ? props.cu_count : 256)) {
+    const int cus = props.cu_count > 0 ? props.cu_count : 256;
+    if (f64 && f64_dma_fits(M, N, K, cus)) {
+        plan->implementation = "gfx950_mfma_f64_16x16x4_lds_dma";
+        plan->threads = 256;
+        plan->grid = (int)((M / kF64BM) * (N / kF64BN));
+        plan->tile_m = kF64BM;
+        plan->tile_n = kF64BN;
+        plan->tile_k = kF64StageK;
+        plan->wave_grid_m = plan->wave_grid_n = 2;
+        plan->frag_m = plan->frag_n = 16;
+        plan->frag_k = 4;
+        plan->wave_tile_m = 8;
+        plan->wave_tile_n = 4;
+        plan->k_stages = kF64Stages;
+        plan->split_k = 1;
+        plan->tile_group_m = kF32GroupM;
+        plan->workspace = 0;
+        plan->variant = kVariantHighp;
+        plan->config = 1;
+        return MB_OK;
+    }
+    if (!f64 && f32_dma_fits(M, N, K, cus)) {
         plan->implementation = "gfx950_mfma_f32_32x32x2_lds_dma";
         plan->threads = 256;
         plan->grid = (int)((M / kF32Tile) * (N / kF32Tile));
@@ -438,7 +585,16 @@ int gemm_highp_launch(int dtype, const void* A, const void* B, void* C, int64_t 
                 return MB_OK;
             }
             return launch_typed<float>(A, B, C, M, N, K, stream);
-        case MB_DT_FLOAT64: return launch_typed<double>(A, B, C, M, N, K, stream);
+        case MB_DT_FLOAT64:
+            if (plan.config == 1) {
+                const int tiles_m = (int)(M / kF64BM), tiles_n = (int)(N / kF64BN);
+                hipLaunchKernelGGL(gemm_f64_dma_kernel, dim3(tiles_m * tiles_n), dim3(256), 0, stream,
+                                   static_cast<const double*>(A), static_cast<const double*>(B),
+                                   static_cast<double*>(C), (int)M, (int)N, (int)K, tiles_m, tiles_n);
+                MB_HIP_TRY(hipGetLastError());
+                return MB_OK;
+            }
+            return launch_typed<double>(A, B, C, M, N, K, stream);
         default:
             set_error("fp32/fp64 GEMM: unsupported dtype %d", dtype);
             return MB_ERR_UNSUPPORTED;

@@ -309,6 +309,44 @@ def test_f32_lds_dma_against_float64_brute_force(lib, shape, monkeypatch):
     assert torch.all((staged - ref).abs() <= bound)
 
 
+@pytest.mark.parametrize("shape, dma", [((4096, 8192, 64), True), ((8192, 4096, 40), True), ((2048, 2048, 2048), False),
+                                        ((4096, 8192, 60), False), ((4096, 8000, 64), False)])
+def test_f64_lds_dma_kernel_selection(lib, shape, dma):
+    # fp64 takes the LDS-DMA kernel for whole 256 x 128 tiles, K in steps of 8 and at least one tile per CU.
+    info = lib.gemm_info(capi.DT_FLOAT64, *shape)
+    assert (info["implementation"] == "gfx950_mfma_f64_16x16x4_lds_dma") == dma
+    assert (info["tile_m"], info["tile_n"]) == ((256, 128) if dma else (128, 128))
+
+
+@pytest.mark.parametrize("shape", [(4096, 8192, 40), (8192, 4096, 24)])
+def test_f64_lds_dma_against_float64_brute_force(lib, shape, monkeypatch):
+    # K permuted inside each stage (lane group g takes K 2g + t at step t); every element within the
+    # fp64 accumulation bound of the brute force, and the staged kernel (forced) within the same bound.
+    m, n, k = shape
+    assert lib.gemm_info(capi.DT_FLOAT64, m, n, k)["implementation"] == "gfx950_mfma_f64_16x16x4_lds_dma"
+    print(f"[gemm] f64 lds-dma {shape}", flush=True)
+    ops = rp.gemm_inputs(m, n, k, "float64", seed=6)
+    got = _gemm(lib, "float64", ops["a"], ops["b"])
+    a64, b64 = ops["a"].numpy(), ops["b"].numpy()
+    ref = torch.from_numpy(clib.gemm_f64(a64, b64))
+    mag = torch.from_numpy(np.abs(a64)) @ torch.from_numpy(np.abs(b64))
+    bound = ref.abs() * UNIT["float64"] + (k + 1) * UNIT["float64"] * mag
+    assert torch.all((got - ref).abs() <= bound)
+    monkeypatch.setenv("MB_GEMM_HIGHP_REGISTER", "1")
+    assert lib.gemm_info(capi.DT_FLOAT64, m, n, k)["implementation"] == "gfx950_mfma_f64_16x16x4"
+    staged = _gemm(lib, "float64", ops["a"], ops["b"])
+    assert torch.all((staged - ref).abs() <= bound)
+
+
+def test_f64_lds_dma_constant_fill_is_exact(lib):
+    m, n, k = 4096, 8192, 1024
+    a = torch.full((m, k), 0.03125, dtype=torch.float64)
+    b = torch.full((k, n), 0.03125, dtype=torch.float64)
+    assert lib.gemm_info(capi.DT_FLOAT64, m, n, k)["implementation"] == "gfx950_mfma_f64_16x16x4_lds_dma"
+    got = _gemm(lib, "float64", a, b)
+    assert torch.all(got == k / 1024)
+
+
 def test_f32_lds_dma_constant_fill_is_exact(lib):
     # The reference executable's constant fill: A = B = 0.03125 gives C = K / 1024 exactly.
     m, n, k = 4096, 4096, 1024
