@@ -289,43 +289,59 @@ gemm_f32_dma_kernel(const float* __restrict__ A, const float* __restrict__ B, fl
     for (int st = 0; st < kF32Stages - 1; ++st) issue(min(st, last), st);
     const int a_row = wm * 128 + (lane & 31);
     const int b_col = wn * 128 + (lane & 31);
-    for (int kt = 0; kt < ksteps; ++kt) {
-        // Stage kt has landed for every wave, and every wave has finished
-        // reading the slot of stage kt - 1, which takes stage kt + 3's loads
-        // (past the last stage they repeat it: in bounds, never read).
-        wait_vmcnt_and_barrier<kF32Loads * (kF32Stages - 2)>();
-        issue(min(kt + kF32Stages - 1, last), (kt + kF32Stages - 1) % kF32Stages);
+    // A operands: a[i][t] is K 8h + t of fragment i's row. Steps 0-3 use the
+    // first 16-byte chunk, steps 4-7 the second, so the next stage's first
+    // chunk is read into the registers steps 0-3 are done with (after the
+    // mid-stage barrier) and its second chunk at the stage boundary, four
+    // steps before it is needed: one register set.
+    float a[4][8];
+    float b[2][4];     // B operands of this step and the next
+    auto read_a = [&](int kt, int e) {
         const unsigned char* slot = ring[kt % kF32Stages];
-        const unsigned char* sb = slot + kF32ABytes;
-        float a[4][8];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int row = a_row + 32 * i;
+            // Whole float vectors: __builtin_bit_cast of a single ext_vector
+            // element (bit_cast(float, v[w]) on a u32x4) is miscompiled by this
+            // clang -- it reuses element 0 and drops the other loads.
+            const f32x4 v = *reinterpret_cast<const f32x4*>(slot + row * 64 + (((2 * half + e) ^ swz_a(row)) << 4));
 #pragma unroll
-            for (int e = 0; e < 2; ++e) {
-                // Read as whole float vectors: __builtin_bit_cast of a single
-                // ext_vector element (bit_cast(float, v[w]) on a u32x4) is
-                // miscompiled by this clang -- it reuses element 0 and drops
-                // the other loads.
-                const f32x4 v = *reinterpret_cast<const f32x4*>(slot + row * 64 + (((2 * half + e) ^ swz_a(row)) << 4));
-#pragma unroll
-                for (int w = 0; w < 4; ++w) a[i][4 * e + w] = v[w];
-            }
+            for (int w = 0; w < 4; ++w) a[i][4 * e + w] = v[w];
         }
-        float b[2][4];
-        auto read_b = [&](int t, int set) {
-            const int row = 8 * half + t;
+    };
+    auto read_b = [&](int kt, int t, int set) {
+        const unsigned char* sb = ring[kt % kF32Stages] + kF32ABytes;
+        const int row = 8 * half + t;
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int col = b_col + 32 * j;
-                b[set][j] = *reinterpret_cast<const float*>(sb + row * kF32BRow + (((col >> 2) ^ swz_b32(row)) << 4) +
-                                                            4 * (col & 3));
+        for (int j = 0; j < 4; ++j) {
+            const int col = b_col + 32 * j;
+            b[set][j] =
+                *reinterpret_cast<const float*>(sb + row * kF32BRow + (((col >> 2) ^ swz_b32(row)) << 4) + 4 * (col & 3));
+        }
+    };
+    // One barrier per stage, at its middle: it certifies that stage kt + 1 has
+    // landed for every wave and that every wave is done with stage kt - 1's
+    // slot, which takes stage kt + 3's loads. The next stage's operands are
+    // read under this stage's MFMAs (A's first chunk after the barrier, its
+    // first B operands in the last step, A's second chunk at the boundary), so
+    // a stage boundary has no wait. Past the last stage the loads repeat it (in
+    // bounds, never used).
+    constexpr int kSteps = kF32StageK / 2, kMid = kSteps / 2;
+    wait_vmcnt_and_barrier<kF32Loads * (kF32Stages - 2)>();
+    read_a(0, 0);
+    read_a(0, 1);
+    read_b(0, 0, 0);
+    for (int kt = 0; kt < ksteps; ++kt) {
+#pragma unroll
+        for (int t = 0; t < kSteps; ++t) {
+            if (t == 0 && kt > 0) read_a(kt, 1);
+            if (t == kMid) {
+                wait_vmcnt_and_barrier<kF32Loads * (kF32Stages - 3)>();
+                issue(min(kt + kF32Stages - 1, last), (kt + kF32Stages - 1) % kF32Stages);
+                read_a(kt + 1, 0);
             }
-        };
-        read_b(0, 0);
-#pragma unroll
-        for (int t = 0; t < kF32StageK / 2; ++t) {
-            if (t + 1 < kF32StageK / 2) read_b(t + 1, (t + 1) & 1);
+            if (t + 1 < kSteps) read_b(kt, t + 1, (t + 1) & 1);
+            else read_b(kt + 1, 0, 0);
             __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int i = 0; i < 4; ++i)
@@ -426,37 +442,58 @@ gemm_f64_dma_kernel(const double* __restrict__ A, const double* __restrict__ B, 
     for (int st = 0; st < kF64Stages - 1; ++st) issue(min(st, last), st);
     const int a_row = wm * 128 + (lane & 15);
     const int b_col = wn * 64 + (lane & 15);
-    for (int kt = 0; kt < ksteps; ++kt) {
-        wait_vmcnt_and_barrier<kF64Loads * (kF64Stages - 2)>();
-        issue(min(kt + kF64Stages - 1, last), (kt + kF64Stages - 1) % kF64Stages);
+    double a[2][8][2];  // A operands of this stage and the next
+    double b[2][4];     // B operands of this step and the next
+    auto read_a = [&](int kt, auto setc) {
+        constexpr int set = decltype(setc)::value;
         const unsigned char* slot = ring[kt % kF64Stages];
-        const unsigned char* sb = slot + kF64ABytes;
-        double a[8][2];
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
             const int row = a_row + 16 * i;
             const f64x2 v = *reinterpret_cast<const f64x2*>(slot + row * 64 + ((grp ^ swz_a(row)) << 4));
-            a[i][0] = v[0];
-            a[i][1] = v[1];
+            a[set][i][0] = v[0];
+            a[set][i][1] = v[1];
         }
-        double b[2][4];
+    };
+    auto read_b = [&](int kt, int t, int set) {
+        const unsigned char* sb = ring[kt % kF64Stages] + kF64ABytes;
+        const int row = 2 * grp + t;
 #pragma unroll
-        for (int t = 0; t < kF64StageK / 4; ++t) {
-            const int row = 2 * grp + t;
+        for (int j = 0; j < 4; ++j) {
+            const int col = b_col + 16 * j;
+            b[set][j] = *reinterpret_cast<const double*>(sb + row * kF64BRow + (((col >> 1) ^ swz_b64(row)) << 4) +
+                                                         8 * (col & 1));
+        }
+    };
+    // The fp32 kernel's schedule: one barrier per stage, between its two
+    // steps, after which stage kt + 1's A operands are read under the second
+    // step's MFMAs and its first B operands at the end of the stage.
+    auto stage = [&](int kt, auto curc) {
+        constexpr int cur = decltype(curc)::value;
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int col = b_col + 16 * j;
-                b[t][j] = *reinterpret_cast<const double*>(sb + row * kF64BRow + (((col >> 1) ^ swz_b64(row)) << 4) +
-                                                           8 * (col & 1));
+        for (int t = 0; t < 2; ++t) {
+            if (t == 1) {
+                wait_vmcnt_and_barrier<kF64Loads * (kF64Stages - 3)>();
+                issue(min(kt + kF64Stages - 1, last), (kt + kF64Stages - 1) % kF64Stages);
+                read_a(kt + 1, std::integral_constant<int, cur ^ 1>{});
+                read_b(kt + 1, 0, 0);
+            } else {
+                read_b(kt, 1, 1);
             }
-        }
-#pragma unroll
-        for (int t = 0; t < kF64StageK / 4; ++t)
+            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int i = 0; i < 8; ++i)
 #pragma unroll
                 for (int j = 0; j < 4; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f64_16x16x4f64(a[i][t], b[t][j], acc[i][j], 0, 0, 0);
+                    acc[i][j] = __builtin_amdgcn_mfma_f64_16x16x4f64(a[cur][i][t], b[t][j], acc[i][j], 0, 0, 0);
+        }
+    };
+    wait_vmcnt_and_barrier<kF64Loads * (kF64Stages - 2)>();
+    read_a(0, std::integral_constant<int, 0>{});
+    read_b(0, 0, 0);
+    for (int kt = 0; kt < ksteps; kt += 2) {
+        stage(kt, std::integral_constant<int, 0>{});
+        if (kt + 1 < ksteps) stage(kt + 1, std::integral_constant<int, 1>{});
     }
     wait_vmcnt_and_barrier<0>();
 
