@@ -3,12 +3,17 @@
 // accumulated in that type by the MFMAs (fp32: v_mfma_f32_32x32x2_f32; fp64:
 // v_mfma_f64_16x16x4_f64), for any M, N, K >= 1.
 //
-// These MFMAs deliver 1/16 (fp32) and 1/32 (fp64) of the bf16 rate, so a
-// 128 x 128 block tile with 64 bytes of K per stage already needs far less
-// LDS and L2 bandwidth than the units can use; the kernel keeps the plain
-// structure: operands come through registers into a double-buffered LDS tile
-// (one barrier per stage), and the next stage's global loads are in flight
-// while the current stage's MFMAs run.
+// Two kernels. Shapes made of whole 256 x 256 (fp32) or 256 x 128 (fp64)
+// tiles with at least one tile per CU run on an LDS-DMA ring like the 16-bit
+// pipelined kernel (gemm_f32_dma_kernel, gemm_f64_dma_kernel below: 92% and
+// 88% of peak at 8192^3). Every other shape runs the register-staged kernel
+// that follows, which takes any shape and stays near 80% of peak:
+//
+// Register-staged kernel. Operands come through registers into a
+// double-buffered LDS tile (one barrier per stage), and the next stage's
+// global loads are in flight while the current stage's MFMAs run. A 128 x 128
+// block tile with 64 bytes of K per stage, 4 waves in a 2 x 2 grid owning
+// 64 x 64 of C each.
 //
 // LDS layout per stage: A transposed to [BK][BM + pad] (the MFMA hands each
 // lane one A row at a fixed k, so consecutive lanes read consecutive
@@ -16,8 +21,7 @@
 // rows first, so the transposing stores of a wave also go to 64 consecutive
 // rows of one k. The 128-byte pad puts the lanes that
 // read the next k (fp32: lanes 32-63; fp64: every other group of 16) on the
-// other half of the 64 banks, so operand reads are conflict-free. 4 waves in
-// a 2 x 2 grid own 64 x 64 of C each.
+// other half of the 64 banks, so operand reads are conflict-free.
 //
 // Global loads move 16 bytes per lane when the row pitches keep 16-byte
 // alignment (K and N multiples of 16 / elem bytes); otherwise element-wise.
