@@ -231,22 +231,20 @@ gemm_highp_kernel(const T* __restrict__ A, const T* __restrict__ B, T* __restric
 // fragment hold one C row, 4 runs of 4 consecutive columns; the epilogue
 // stores them as 16-byte pieces straight from registers (a tile computes for
 // milliseconds; its 256 KiB of C do not need LDS staging).
-constexpr int kF32Tile = 256, kF32Stages = 4, kF32StageK = 16;
-constexpr int kF32ABytes = kF32Tile * 64;                  // [256 rows][64 B]
-constexpr int kF32BRow = kF32Tile * 4;                     // 1024 B
-constexpr int kF32BBytes = kF32StageK * kF32BRow;          // [16 rows][1024 B]
-constexpr int kF32Slot = kF32ABytes + kF32BBytes;          // 32 KiB
-constexpr int kF32AInstr = kF32ABytes / 1024 / 4;          // DMA instructions per wave per stage
-constexpr int kF32BInstr = kF32BBytes / 1024 / 4;
-constexpr int kF32Loads = kF32AInstr + kF32BInstr;
-constexpr int kF32GroupM = 4;
+constexpr int kF32Stages = 4, kF32StageK = 16, kF32GroupM = 4;
 
 __device__ __forceinline__ int swz_b32(int row) { return ((row >> 3) & 1) << 3; }
 
+template <int BM, int BN>
 __global__ void __launch_bounds__(256)
 gemm_f32_dma_kernel(const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ C, int M, int N,
                     int K, int tiles_m, int tiles_n) {
-    __shared__ __attribute__((aligned(1024))) unsigned char ring[kF32Stages][kF32Slot];
+    // Per-tile sizes: waves in a 2 x 2 grid, fragments of 32 x 32.
+    constexpr int WTM = BM / 2, WTN = BN / 2, FM = WTM / 32, FN = WTN / 32;
+    constexpr int ABytes = BM * 64, BRow = BN * 4, BBytes = kF32StageK * BRow, Slot = ABytes + BBytes;
+    constexpr int AInstr = ABytes / 1024 / 4, BInstr = BBytes / 1024 / 4, Loads = AInstr + BInstr;
+    static_assert(AInstr >= 1 && BInstr >= 1 && WTM % 32 == 0 && WTN % 32 == 0 && BRow >= 256, "tile shape");
+    __shared__ __attribute__((aligned(1024))) unsigned char ring[kF32Stages][Slot];
     const int tid = threadIdx.x, lane = tid & 63, half = lane >> 5;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave >> 1, wn = wave & 1;
@@ -254,56 +252,56 @@ gemm_f32_dma_kernel(const float* __restrict__ A, const float* __restrict__ B, fl
     tile_coords((int)blockIdx.x, tiles_m * tiles_n, tiles_m, tiles_n, kF32GroupM, &tm, &tn);
     const int lda = K * 4, ldb = N * 4;
     const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<float*>(A) + (int64_t)tm * kF32Tile * K, (short)0, kF32Tile * lda, kBufferFlags);
+        const_cast<float*>(A) + (int64_t)tm * BM * K, (short)0, BM * lda, kBufferFlags);
     const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<float*>(B) + (int64_t)tn * kF32Tile, (short)0, K * ldb, kBufferFlags);
-    int a_voff[kF32AInstr], b_voff[kF32BInstr];
+        const_cast<float*>(B) + (int64_t)tn * BN, (short)0, K * ldb, kBufferFlags);
+    int a_voff[AInstr], b_voff[BInstr];
 #pragma unroll
-    for (int q = 0; q < kF32AInstr; ++q) {
-        const int lin = (wave * kF32AInstr + q) * 1024 + lane * 16;
+    for (int q = 0; q < AInstr; ++q) {
+        const int lin = (wave * AInstr + q) * 1024 + lane * 16;
         const int row = lin / 64, pchunk = (lin % 64) >> 4;
         a_voff[q] = row * lda + ((pchunk ^ swz_a(row)) << 4);
     }
 #pragma unroll
-    for (int q = 0; q < kF32BInstr; ++q) {
-        const int lin = (wave * kF32BInstr + q) * 1024 + lane * 16;
-        const int row = lin / kF32BRow, pchunk = (lin % kF32BRow) >> 4;
+    for (int q = 0; q < BInstr; ++q) {
+        const int lin = (wave * BInstr + q) * 1024 + lane * 16;
+        const int row = lin / BRow, pchunk = (lin % BRow) >> 4;
         b_voff[q] = row * ldb + ((pchunk ^ swz_b32(row)) << 4);
     }
     auto issue = [&](int kt, int slot) {
         const unsigned base = (unsigned)(uintptr_t)(MB_LDS unsigned char*)ring[slot];
 #pragma unroll
-        for (int q = 0; q < kF32AInstr; ++q)
-            lds_dma16(ra, base + (wave * kF32AInstr + q) * 1024, a_voff[q], kt * 64);
+        for (int q = 0; q < AInstr; ++q)
+            lds_dma16(ra, base + (wave * AInstr + q) * 1024, a_voff[q], kt * 64);
 #pragma unroll
-        for (int q = 0; q < kF32BInstr; ++q)
-            lds_dma16(rb, base + kF32ABytes + (wave * kF32BInstr + q) * 1024, b_voff[q], kt * kF32StageK * ldb);
+        for (int q = 0; q < BInstr; ++q)
+            lds_dma16(rb, base + ABytes + (wave * BInstr + q) * 1024, b_voff[q], kt * kF32StageK * ldb);
     };
 
-    f32x16 acc[4][4];
+    f32x16 acc[FM][FN];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < FM; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
+        for (int j = 0; j < FN; ++j)
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
     const int ksteps = K / kF32StageK, last = ksteps - 1;
 #pragma unroll
     for (int st = 0; st < kF32Stages - 1; ++st) issue(min(st, last), st);
-    const int a_row = wm * 128 + (lane & 31);
-    const int b_col = wn * 128 + (lane & 31);
+    const int a_row = wm * WTM + (lane & 31);
+    const int b_col = wn * WTN + (lane & 31);
     // A operands: a[i][t] is K 8h + t of fragment i's row. Steps 0-3 use the
     // first 16-byte chunk, steps 4-7 the second, so the next stage's first
     // chunk is read into the registers steps 0-3 are done with (after the
     // mid-stage barrier) and its second chunk at the stage boundary, four
     // steps before it is needed: one register set.
-    float a[4][8];
-    float b[2][4];     // B operands of this step and the next
+    float a[FM][8];
+    float b[2][FN];     // B operands of this step and the next
     auto read_a = [&](int kt, int e) {
         const unsigned char* slot = ring[kt % kF32Stages];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
+        for (int i = 0; i < FM; ++i) {
             const int row = a_row + 32 * i;
             // Whole float vectors: __builtin_bit_cast of a single ext_vector
             // element (bit_cast(float, v[w]) on a u32x4) is miscompiled by this
@@ -314,13 +312,13 @@ gemm_f32_dma_kernel(const float* __restrict__ A, const float* __restrict__ B, fl
         }
     };
     auto read_b = [&](int kt, int t, int set) {
-        const unsigned char* sb = ring[kt % kF32Stages] + kF32ABytes;
+        const unsigned char* sb = ring[kt % kF32Stages] + ABytes;
         const int row = 8 * half + t;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
+        for (int j = 0; j < FN; ++j) {
             const int col = b_col + 32 * j;
             b[set][j] =
-                *reinterpret_cast<const float*>(sb + row * kF32BRow + (((col >> 2) ^ swz_b32(row)) << 4) + 4 * (col & 3));
+                *reinterpret_cast<const float*>(sb + row * BRow + (((col >> 2) ^ swz_b32(row)) << 4) + 4 * (col & 3));
         }
     };
     // One barrier per stage, at its middle: it certifies that stage kt + 1 has
@@ -331,7 +329,7 @@ gemm_f32_dma_kernel(const float* __restrict__ A, const float* __restrict__ B, fl
     // a stage boundary has no wait. Past the last stage the loads repeat it (in
     // bounds, never used).
     constexpr int kSteps = kF32StageK / 2, kMid = kSteps / 2;
-    wait_vmcnt_and_barrier<kF32Loads * (kF32Stages - 2)>();
+    wait_vmcnt_and_barrier<Loads * (kF32Stages - 2)>();
     read_a(0, 0);
     read_a(0, 1);
     read_b(0, 0, 0);
@@ -340,7 +338,7 @@ gemm_f32_dma_kernel(const float* __restrict__ A, const float* __restrict__ B, fl
         for (int t = 0; t < kSteps; ++t) {
             if (t == 0 && kt > 0) read_a(kt, 1);
             if (t == kMid) {
-                wait_vmcnt_and_barrier<kF32Loads * (kF32Stages - 3)>();
+                wait_vmcnt_and_barrier<Loads * (kF32Stages - 3)>();
                 issue(min(kt + kF32Stages - 1, last), (kt + kF32Stages - 1) % kF32Stages);
                 read_a(kt + 1, 0);
             }
@@ -348,9 +346,9 @@ gemm_f32_dma_kernel(const float* __restrict__ A, const float* __restrict__ B, fl
             else read_b(kt + 1, 0, 0);
             __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
+            for (int i = 0; i < FM; ++i)
 #pragma unroll
-                for (int j = 0; j < 4; ++j)
+                for (int j = 0; j < FN; ++j)
                     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(b[t & 1][j], a[i][t], acc[i][j], 0, 0, 0);
         }
     }
@@ -359,11 +357,11 @@ gemm_f32_dma_kernel(const float* __restrict__ A, const float* __restrict__ B, fl
     // Accumulator register 4g + q of lane l holds C[row 32i + l % 32]
     // [col 32j + 8g + 4 * (l / 32) + q] of the wave's tile.
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        float* crow = C + (int64_t)(tm * kF32Tile + wm * 128 + 32 * i + (lane & 31)) * N + tn * kF32Tile + wn * 128 +
+    for (int i = 0; i < FM; ++i) {
+        float* crow = C + (int64_t)(tm * BM + wm * WTM + 32 * i + (lane & 31)) * N + tn * BN + wn * WTN +
                       4 * half;
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
+        for (int j = 0; j < FN; ++j)
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
                 const f32x4 v = {acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]};
@@ -385,21 +383,20 @@ gemm_f32_dma_kernel(const float* __restrict__ A, const float* __restrict__ B, fl
 // 8 x 4 fragments (256 accumulator registers); A is the MFMA's first operand,
 // so accumulator r of lane l is C row 4r + l / 16, column l % 16, and a store
 // instruction writes 4 rows x 128 bytes straight from registers.
-constexpr int kF64BM = 256, kF64BN = 128, kF64Stages = 4, kF64StageK = 8;
-constexpr int kF64ABytes = kF64BM * 64;                    // [256 rows][64 B]
-constexpr int kF64BRow = kF64BN * 8;                       // 1024 B
-constexpr int kF64BBytes = kF64StageK * kF64BRow;          // [8 rows][1024 B]
-constexpr int kF64Slot = kF64ABytes + kF64BBytes;          // 24 KiB
-constexpr int kF64AInstr = kF64ABytes / 1024 / 4;
-constexpr int kF64BInstr = kF64BBytes / 1024 / 4;
-constexpr int kF64Loads = kF64AInstr + kF64BInstr;
+constexpr int kF64Stages = 4, kF64StageK = 8;
 
 __device__ __forceinline__ int swz_b64(int row) { return ((row >> 1) & 1) << 3; }
 
+template <int BM, int BN>
 __global__ void __launch_bounds__(256)
 gemm_f64_dma_kernel(const double* __restrict__ A, const double* __restrict__ B, double* __restrict__ C, int M,
                     int N, int K, int tiles_m, int tiles_n) {
-    __shared__ __attribute__((aligned(1024))) unsigned char ring[kF64Stages][kF64Slot];
+    // Per-tile sizes: waves in a 2 x 2 grid, fragments of 16 x 16.
+    constexpr int WTM = BM / 2, WTN = BN / 2, FM = WTM / 16, FN = WTN / 16;
+    constexpr int ABytes = BM * 64, BRow = BN * 8, BBytes = kF64StageK * BRow, Slot = ABytes + BBytes;
+    constexpr int AInstr = ABytes / 1024 / 4, BInstr = BBytes / 1024 / 4, Loads = AInstr + BInstr;
+    static_assert(AInstr >= 1 && BInstr >= 1 && WTM % 16 == 0 && WTN % 16 == 0 && BRow >= 256, "tile shape");
+    __shared__ __attribute__((aligned(1024))) unsigned char ring[kF64Stages][Slot];
     const int tid = threadIdx.x, lane = tid & 63, grp = lane >> 4;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave >> 1, wn = wave & 1;
@@ -407,52 +404,52 @@ gemm_f64_dma_kernel(const double* __restrict__ A, const double* __restrict__ B, 
     tile_coords((int)blockIdx.x, tiles_m * tiles_n, tiles_m, tiles_n, kF32GroupM, &tm, &tn);
     const int lda = K * 8, ldb = N * 8;
     const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<double*>(A) + (int64_t)tm * kF64BM * K, (short)0, kF64BM * lda, kBufferFlags);
+        const_cast<double*>(A) + (int64_t)tm * BM * K, (short)0, BM * lda, kBufferFlags);
     const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<double*>(B) + (int64_t)tn * kF64BN, (short)0, K * ldb, kBufferFlags);
-    int a_voff[kF64AInstr], b_voff[kF64BInstr];
+        const_cast<double*>(B) + (int64_t)tn * BN, (short)0, K * ldb, kBufferFlags);
+    int a_voff[AInstr], b_voff[BInstr];
 #pragma unroll
-    for (int q = 0; q < kF64AInstr; ++q) {
-        const int lin = (wave * kF64AInstr + q) * 1024 + lane * 16;
+    for (int q = 0; q < AInstr; ++q) {
+        const int lin = (wave * AInstr + q) * 1024 + lane * 16;
         const int row = lin / 64, pchunk = (lin % 64) >> 4;
         a_voff[q] = row * lda + ((pchunk ^ swz_a(row)) << 4);
     }
 #pragma unroll
-    for (int q = 0; q < kF64BInstr; ++q) {
-        const int lin = (wave * kF64BInstr + q) * 1024 + lane * 16;
-        const int row = lin / kF64BRow, pchunk = (lin % kF64BRow) >> 4;
+    for (int q = 0; q < BInstr; ++q) {
+        const int lin = (wave * BInstr + q) * 1024 + lane * 16;
+        const int row = lin / BRow, pchunk = (lin % BRow) >> 4;
         b_voff[q] = row * ldb + ((pchunk ^ swz_b64(row)) << 4);
     }
     auto issue = [&](int kt, int slot) {
         const unsigned base = (unsigned)(uintptr_t)(MB_LDS unsigned char*)ring[slot];
 #pragma unroll
-        for (int q = 0; q < kF64AInstr; ++q)
-            lds_dma16(ra, base + (wave * kF64AInstr + q) * 1024, a_voff[q], kt * 64);
+        for (int q = 0; q < AInstr; ++q)
+            lds_dma16(ra, base + (wave * AInstr + q) * 1024, a_voff[q], kt * 64);
 #pragma unroll
-        for (int q = 0; q < kF64BInstr; ++q)
-            lds_dma16(rb, base + kF64ABytes + (wave * kF64BInstr + q) * 1024, b_voff[q], kt * kF64StageK * ldb);
+        for (int q = 0; q < BInstr; ++q)
+            lds_dma16(rb, base + ABytes + (wave * BInstr + q) * 1024, b_voff[q], kt * kF64StageK * ldb);
     };
 
-    f64x4 acc[8][4];
+    f64x4 acc[FM][FN];
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
+    for (int i = 0; i < FM; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
+        for (int j = 0; j < FN; ++j)
 #pragma unroll
             for (int r = 0; r < 4; ++r) acc[i][j][r] = 0.0;
 
     const int ksteps = K / kF64StageK, last = ksteps - 1;
 #pragma unroll
     for (int st = 0; st < kF64Stages - 1; ++st) issue(min(st, last), st);
-    const int a_row = wm * 128 + (lane & 15);
-    const int b_col = wn * 64 + (lane & 15);
-    double a[2][8][2];  // A operands of this stage and the next
-    double b[2][4];     // B operands of this step and the next
+    const int a_row = wm * WTM + (lane & 15);
+    const int b_col = wn * WTN + (lane & 15);
+    double a[2][FM][2];  // A operands of this stage and the next
+    double b[2][FN];     // B operands of this step and the next
     auto read_a = [&](int kt, auto setc) {
         constexpr int set = decltype(setc)::value;
         const unsigned char* slot = ring[kt % kF64Stages];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
+        for (int i = 0; i < FM; ++i) {
             const int row = a_row + 16 * i;
             const f64x2 v = *reinterpret_cast<const f64x2*>(slot + row * 64 + ((grp ^ swz_a(row)) << 4));
             a[set][i][0] = v[0];
@@ -460,12 +457,12 @@ gemm_f64_dma_kernel(const double* __restrict__ A, const double* __restrict__ B, 
         }
     };
     auto read_b = [&](int kt, int t, int set) {
-        const unsigned char* sb = ring[kt % kF64Stages] + kF64ABytes;
+        const unsigned char* sb = ring[kt % kF64Stages] + ABytes;
         const int row = 2 * grp + t;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
+        for (int j = 0; j < FN; ++j) {
             const int col = b_col + 16 * j;
-            b[set][j] = *reinterpret_cast<const double*>(sb + row * kF64BRow + (((col >> 1) ^ swz_b64(row)) << 4) +
+            b[set][j] = *reinterpret_cast<const double*>(sb + row * BRow + (((col >> 1) ^ swz_b64(row)) << 4) +
                                                          8 * (col & 1));
         }
     };
@@ -477,7 +474,7 @@ gemm_f64_dma_kernel(const double* __restrict__ A, const double* __restrict__ B, 
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
             if (t == 1) {
-                wait_vmcnt_and_barrier<kF64Loads * (kF64Stages - 3)>();
+                wait_vmcnt_and_barrier<Loads * (kF64Stages - 3)>();
                 issue(min(kt + kF64Stages - 1, last), (kt + kF64Stages - 1) % kF64Stages);
                 read_a(kt + 1, std::integral_constant<int, cur ^ 1>{});
                 read_b(kt + 1, 0, 0);
@@ -486,13 +483,13 @@ gemm_f64_dma_kernel(const double* __restrict__ A, const double* __restrict__ B, 
             }
             __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-            for (int i = 0; i < 8; ++i)
+            for (int i = 0; i < FM; ++i)
 #pragma unroll
-                for (int j = 0; j < 4; ++j)
+                for (int j = 0; j < FN; ++j)
                     acc[i][j] = __builtin_amdgcn_mfma_f64_16x16x4f64(a[cur][i][t], b[t][j], acc[i][j], 0, 0, 0);
         }
     };
-    wait_vmcnt_and_barrier<kF64Loads * (kF64Stages - 2)>();
+    wait_vmcnt_and_barrier<Loads * (kF64Stages - 2)>();
     read_a(0, std::integral_constant<int, 0>{});
     read_b(0, 0, 0);
     for (int kt = 0; kt < ksteps; kt += 2) {
@@ -502,32 +499,51 @@ gemm_f64_dma_kernel(const double* __restrict__ A, const double* __restrict__ B, 
     wait_vmcnt_and_barrier<0>();
 
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
+    for (int i = 0; i < FM; ++i)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            double* crow = C + (int64_t)(tm * kF64BM + wm * 128 + 16 * i + 4 * r + grp) * N + tn * kF64BN + wn * 64 +
+            double* crow = C + (int64_t)(tm * BM + wm * WTM + 16 * i + 4 * r + grp) * N + tn * BN + wn * WTN +
                            (lane & 15);
 #pragma unroll
-            for (int j = 0; j < 4; ++j) crow[16 * j] = acc[i][j][r];
+            for (int j = 0; j < FN; ++j) crow[16 * j] = acc[i][j][r];
         }
 }
 
-bool f64_dma_fits(int64_t M, int64_t N, int64_t K, int cus) {
-    if (std::getenv("MB_GEMM_HIGHP_REGISTER") != nullptr) return false;  // testing override: staged kernel
-    const int64_t tiles = (M / kF64BM) * (N / kF64BN);
-    return M % kF64BM == 0 && N % kF64BN == 0 && K % kF64StageK == 0 && K * N * 8 < (int64_t(1) << 31) &&
-           kF64BM * K * 8 < (int64_t(1) << 31) && tiles <= INT32_MAX && tiles >= cus;
+// Which LDS-DMA ring a shape takes: 1 = the large tile (fp32 256 x 256, fp64
+// 256 x 128) when its tiles cover every CU, 2 = 128 x 128 when the shape
+// divides into it (2048^3 makes 64 large tiles but 256 small ones), 0 = the
+// register-staged kernel. K must be whole stages and the buffer offsets (B's
+// K x N bytes, a 256-row A panel) must stay within 31 bits.
+int highp_dma_config(bool f64, int64_t M, int64_t N, int64_t K, int cus) {
+    if (std::getenv("MB_GEMM_HIGHP_REGISTER") != nullptr) return 0;  // testing override: staged kernel
+    const int64_t e = f64 ? 8 : 4, stage_k = f64 ? kF64StageK : kF32StageK;
+    if (K % stage_k != 0 || K * N * e >= (int64_t(1) << 31) || 256 * K * e >= (int64_t(1) << 31)) return 0;
+    const int64_t bm = 256, bn = f64 ? 128 : 256;
+    if (M % bm == 0 && N % bn == 0 && (M / bm) * (N / bn) >= cus && (M / bm) * (N / bn) <= INT32_MAX) return 1;
+    if (M % 128 == 0 && N % 128 == 0 && (M / 128) * (N / 128) <= INT32_MAX) return 2;
+    return 0;
 }
 
-// Shapes the DMA kernel takes: whole 256 x 256 tiles, K in whole stages,
-// buffer offsets (B's K x N bytes, a 256-row A panel) within 31 bits, and at
-// least one tile per CU -- with fewer (2048^3 makes 64), the staged kernel's
-// 128 x 128 tiles keep more of the GPU busy (2048^3: 98 against 35 TFLOP/s).
-bool f32_dma_fits(int64_t M, int64_t N, int64_t K, int cus) {
-    if (std::getenv("MB_GEMM_HIGHP_REGISTER") != nullptr) return false;  // testing override: staged kernel
-    const int64_t tiles = (M / kF32Tile) * (N / kF32Tile);
-    return M % kF32Tile == 0 && N % kF32Tile == 0 && K % kF32StageK == 0 && K * N * 4 < (int64_t(1) << 31) &&
-           kF32Tile * K * 4 < (int64_t(1) << 31) && tiles <= INT32_MAX && tiles >= cus;
+void highp_dma_tile(bool f64, int cfg, int* bm, int* bn) {
+    *bm = cfg == 1 ? 256 : 128;
+    *bn = cfg == 1 ? (f64 ? 128 : 256) : 128;
+}
+
+template <typename T, int BM, int BN>
+int launch_dma(const void* A, const void* B, void* C, int64_t M, int64_t N, int64_t K, hipStream_t stream) {
+    const int tiles_m = (int)(M / BM), tiles_n = (int)(N / BN);
+    const T* a = static_cast<const T*>(A);
+    const T* b = static_cast<const T*>(B);
+    T* c = static_cast<T*>(C);
+    if constexpr (sizeof(T) == 4) {
+        hipLaunchKernelGGL((gemm_f32_dma_kernel<BM, BN>), dim3(tiles_m * tiles_n), dim3(256), 0, stream, a, b, c,
+                           (int)M, (int)N, (int)K, tiles_m, tiles_n);
+    } else {
+        hipLaunchKernelGGL((gemm_f64_dma_kernel<BM, BN>), dim3(tiles_m * tiles_n), dim3(256), 0, stream, a, b, c,
+                           (int)M, (int)N, (int)K, tiles_m, tiles_n);
+    }
+    MB_HIP_TRY(hipGetLastError());
+    return MB_OK;
 }
 
 template <typename T>
@@ -550,43 +566,27 @@ int launch_typed(const void* A, const void* B, void* C, int64_t M, int64_t N, in
 
 int gemm_highp_plan(int dtype, int64_t M, int64_t N, int64_t K, const DeviceProps& props, GemmPlan* plan) {
     const bool f64 = dtype == MB_DT_FLOAT64;
-    const int cus = props.cu_count > 0 ? props.cu_count : 256;
-    if (f64 && f64_dma_fits(M, N, K, cus)) {
-        plan->implementation = "gfx950_mfma_f64_16x16x4_lds_dma";
+    const int cfg = highp_dma_config(f64, M, N, K, props.cu_count > 0 ? props.cu_count : 256);
+    if (cfg != 0) {
+        int bm, bn;
+        highp_dma_tile(f64, cfg, &bm, &bn);
+        plan->implementation = f64 ? "gfx950_mfma_f64_16x16x4_lds_dma" : "gfx950_mfma_f32_32x32x2_lds_dma";
         plan->threads = 256;
-        plan->grid = (int)((M / kF64BM) * (N / kF64BN));
-        plan->tile_m = kF64BM;
-        plan->tile_n = kF64BN;
-        plan->tile_k = kF64StageK;
+        plan->grid = (int)((M / bm) * (N / bn));
+        plan->tile_m = bm;
+        plan->tile_n = bn;
+        plan->tile_k = f64 ? kF64StageK : kF32StageK;
         plan->wave_grid_m = plan->wave_grid_n = 2;
-        plan->frag_m = plan->frag_n = 16;
-        plan->frag_k = 4;
-        plan->wave_tile_m = 8;
-        plan->wave_tile_n = 4;
-        plan->k_stages = kF64Stages;
+        plan->frag_m = plan->frag_n = f64 ? 16 : 32;
+        plan->frag_k = f64 ? 4 : 2;
+        plan->wave_tile_m = bm / 2 / plan->frag_m;
+        plan->wave_tile_n = bn / 2 / plan->frag_n;
+        plan->k_stages = f64 ? kF64Stages : kF32Stages;
         plan->split_k = 1;
         plan->tile_group_m = kF32GroupM;
         plan->workspace = 0;
         plan->variant = kVariantHighp;
-        plan->config = 1;
-        return MB_OK;
-    }
-    if (!f64 && f32_dma_fits(M, N, K, cus)) {
-        plan->implementation = "gfx950_mfma_f32_32x32x2_lds_dma";
-        plan->threads = 256;
-        plan->grid = (int)((M / kF32Tile) * (N / kF32Tile));
-        plan->tile_m = plan->tile_n = kF32Tile;
-        plan->tile_k = kF32StageK;
-        plan->wave_grid_m = plan->wave_grid_n = 2;
-        plan->frag_m = plan->frag_n = 32;
-        plan->frag_k = 2;
-        plan->wave_tile_m = plan->wave_tile_n = 4;
-        plan->k_stages = kF32Stages;
-        plan->split_k = 1;
-        plan->tile_group_m = kF32GroupM;
-        plan->workspace = 0;
-        plan->variant = kVariantHighp;
-        plan->config = 1;
+        plan->config = cfg;
         return MB_OK;
     }
     const int64_t gx = (N + kHpBN - 1) / kHpBN, gy = (M + kHpBM - 1) / kHpBM;
@@ -617,24 +617,12 @@ int gemm_highp_launch(int dtype, const void* A, const void* B, void* C, int64_t 
                       const GemmPlan& plan, hipStream_t stream) {
     switch (dtype) {
         case MB_DT_FLOAT32:
-            if (plan.config == 1) {
-                const int tiles_m = (int)(M / kF32Tile), tiles_n = (int)(N / kF32Tile);
-                hipLaunchKernelGGL(gemm_f32_dma_kernel, dim3(tiles_m * tiles_n), dim3(256), 0, stream,
-                                   static_cast<const float*>(A), static_cast<const float*>(B), static_cast<float*>(C),
-                                   (int)M, (int)N, (int)K, tiles_m, tiles_n);
-                MB_HIP_TRY(hipGetLastError());
-                return MB_OK;
-            }
+            if (plan.config == 1) return launch_dma<float, 256, 256>(A, B, C, M, N, K, stream);
+            if (plan.config == 2) return launch_dma<float, 128, 128>(A, B, C, M, N, K, stream);
             return launch_typed<float>(A, B, C, M, N, K, stream);
         case MB_DT_FLOAT64:
-            if (plan.config == 1) {
-                const int tiles_m = (int)(M / kF64BM), tiles_n = (int)(N / kF64BN);
-                hipLaunchKernelGGL(gemm_f64_dma_kernel, dim3(tiles_m * tiles_n), dim3(256), 0, stream,
-                                   static_cast<const double*>(A), static_cast<const double*>(B),
-                                   static_cast<double*>(C), (int)M, (int)N, (int)K, tiles_m, tiles_n);
-                MB_HIP_TRY(hipGetLastError());
-                return MB_OK;
-            }
+            if (plan.config == 1) return launch_dma<double, 256, 128>(A, B, C, M, N, K, stream);
+            if (plan.config == 2) return launch_dma<double, 128, 128>(A, B, C, M, N, K, stream);
             return launch_typed<double>(A, B, C, M, N, K, stream);
         default:
             set_error("fp32/fp64 GEMM: unsupported dtype %d", dtype);

@@ -278,17 +278,24 @@ def test_highp_kernel_info(lib, dtype):
     assert info["workspace_bytes"] == 0 and info["tile_m"] == 128
 
 
-@pytest.mark.parametrize("shape, dma", [((4096, 4096, 64), True), ((8192, 2048, 96), True), ((4352, 4096, 16), True),
-                                        ((2048, 2048, 2048), False), ((4096, 4096, 40), False), ((4096, 4000, 64), False)])
-def test_f32_lds_dma_kernel_selection(lib, shape, dma):
-    # fp32 takes the LDS-DMA kernel for whole 256 x 256 tiles, K in steps of 16 and at least one tile
-    # per CU (2048^3 makes 64 and stays on the staged kernel's 128 x 128 tiles).
+@pytest.mark.parametrize("shape, tile", [((4096, 4096, 64), (256, 256)), ((8192, 2048, 96), (256, 256)),
+                                         ((4352, 4096, 16), (256, 256)), ((2048, 2048, 2048), (128, 128)),
+                                         ((1024, 1536, 48), (128, 128)), ((4096, 4096, 40), None),
+                                         ((4096, 4000, 64), None)])
+def test_f32_lds_dma_kernel_selection(lib, shape, tile):
+    # fp32 takes the LDS-DMA ring with 256 x 256 tiles when they cover every CU, else with 128 x 128
+    # tiles when the shape divides (2048^3: 64 large tiles, 256 small); K must be whole stages of 16.
+    # Other shapes keep the register-staged kernel.
     info = lib.gemm_info(capi.DT_FLOAT32, *shape)
-    assert (info["implementation"] == "gfx950_mfma_f32_32x32x2_lds_dma") == dma
-    assert info["tile_m"] == (256 if dma else 128) and info["workspace_bytes"] == 0
+    if tile is None:
+        assert info["implementation"] == "gfx950_mfma_f32_32x32x2" and info["tile_m"] == 128
+    else:
+        assert info["implementation"] == "gfx950_mfma_f32_32x32x2_lds_dma"
+        assert (info["tile_m"], info["tile_n"]) == tile
+    assert info["workspace_bytes"] == 0
 
 
-@pytest.mark.parametrize("shape", [(4096, 4096, 64), (8192, 2048, 96)])
+@pytest.mark.parametrize("shape", [(4096, 4096, 64), (8192, 2048, 96), (1024, 1536, 48), (2048, 2048, 16)])
 def test_f32_lds_dma_against_float64_brute_force(lib, shape, monkeypatch):
     # The LDS-DMA kernel sums each stage's 16 K values in a permuted order (lane half h takes K 8h + t
     # at step t); every element must still sit within the fp32 accumulation bound of an fp64
@@ -309,16 +316,20 @@ def test_f32_lds_dma_against_float64_brute_force(lib, shape, monkeypatch):
     assert torch.all((staged - ref).abs() <= bound)
 
 
-@pytest.mark.parametrize("shape, dma", [((4096, 8192, 64), True), ((8192, 4096, 40), True), ((2048, 2048, 2048), False),
-                                        ((4096, 8192, 60), False), ((4096, 8000, 64), False)])
-def test_f64_lds_dma_kernel_selection(lib, shape, dma):
-    # fp64 takes the LDS-DMA kernel for whole 256 x 128 tiles, K in steps of 8 and at least one tile per CU.
+@pytest.mark.parametrize("shape, tile", [((4096, 8192, 64), (256, 128)), ((8192, 4096, 40), (256, 128)),
+                                         ((2048, 2048, 2048), (128, 128)), ((1024, 1536, 40), (128, 128)),
+                                         ((4096, 8192, 60), None), ((4096, 8000, 64), None)])
+def test_f64_lds_dma_kernel_selection(lib, shape, tile):
+    # fp64: 256 x 128 tiles when they cover every CU, else 128 x 128; K in whole stages of 8.
     info = lib.gemm_info(capi.DT_FLOAT64, *shape)
-    assert (info["implementation"] == "gfx950_mfma_f64_16x16x4_lds_dma") == dma
-    assert (info["tile_m"], info["tile_n"]) == ((256, 128) if dma else (128, 128))
+    if tile is None:
+        assert info["implementation"] == "gfx950_mfma_f64_16x16x4" and info["tile_m"] == 128
+    else:
+        assert info["implementation"] == "gfx950_mfma_f64_16x16x4_lds_dma"
+        assert (info["tile_m"], info["tile_n"]) == tile
 
 
-@pytest.mark.parametrize("shape", [(4096, 8192, 40), (8192, 4096, 24)])
+@pytest.mark.parametrize("shape", [(4096, 8192, 40), (8192, 4096, 24), (1024, 1536, 40), (2048, 2048, 8)])
 def test_f64_lds_dma_against_float64_brute_force(lib, shape, monkeypatch):
     # K permuted inside each stage (lane group g takes K 2g + t at step t); every element within the
     # fp64 accumulation bound of the brute force, and the staged kernel (forced) within the same bound.
