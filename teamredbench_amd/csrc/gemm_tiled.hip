@@ -551,7 +551,10 @@ int gemm_tiled_plan(int dtype, int64_t M, int64_t N, int64_t K, const DeviceProp
                     GemmPlan* plan) {
     const int64_t e = is_fp8(dtype) ? 1 : 2;
     const int64_t stage_k = kStageK / e;
-    if (K % stage_k != 0 || N % 256 != 0) return MB_ERR_SHAPE;
+    // N in 256-column tiles, or for 16-bit inputs in 128-column tiles
+    // (configuration 2; its B rows are 256 bytes, the 16-bit swizzle's width).
+    const bool n128_only = N % 256 != 0;
+    if (K % stage_k != 0 || N % 128 != 0 || (n128_only && e != 2)) return MB_ERR_SHAPE;
     if (K * N * e >= (int64_t(1) << 31) || 256 * K * e >= (int64_t(1) << 31) || M >= (int64_t(1) << 31) ||
         M * N >= (int64_t(1) << 31))
         return MB_ERR_SHAPE;
@@ -563,6 +566,7 @@ int gemm_tiled_plan(int dtype, int64_t M, int64_t N, int64_t K, const DeviceProp
         const int f = std::atoi(force);
         if (f >= 0 && f < kNumConfigs && !(f == 2 && e == 1)) cfg = f;
     }
+    if (n128_only) cfg = 2;
     const bool forced = cfg >= 0;
     if (cfg < 0) cfg = (tiles(0) >= cus && M % kConfigs[0].bm == 0) ? 0 : 1;
     // K splits for problems with too few tiles to fill the GPU, chosen by a

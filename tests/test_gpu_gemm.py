@@ -87,6 +87,26 @@ def test_tiled_configurations(lib, dtype, config, shape, monkeypatch):
 
 
 @pytest.mark.parametrize("dtype", ["bfloat16", "float16"])
+@pytest.mark.parametrize("shape", [(512, 384, 256), (1000, 1152, 320), (64, 640, 512), (16, 1152, 4096), (3, 128, 64)])
+def test_n_multiple_of_128_takes_128x128_tiles(lib, dtype, shape, monkeypatch):
+    # 16-bit shapes with N a multiple of 128 but not 256 run the pipelined kernel on 128 x 128 tiles
+    # (ragged M through the buffer range checks, skinny shapes with K splits).
+    monkeypatch.setenv("MB_GEMM_NO_GEMV", "1")  # keep M <= 4 on the tiled kernel too
+    m, n, k = shape
+    info = lib.gemm_info(capi.DTYPES[dtype], m, n, k)
+    assert info["implementation"] == "gfx950_mfma32_lds_dma" and (info["tile_m"], info["tile_n"]) == (128, 128)
+    print(f"[gemm] n%128 {dtype} {shape} split {info['split_k']}", flush=True)
+    _check_random(lib, dtype, m, n, k, seed=n + 3)
+
+
+@pytest.mark.parametrize("dtype", ["float8_e4m3fn", "float8_e5m2"])
+def test_fp8_n_multiple_of_128_only_uses_the_generic_kernel(lib, dtype):
+    info = lib.gemm_info(capi.DTYPES[dtype], 512, 384, 256)
+    assert info["implementation"] != "gfx950_mfma32_lds_dma"
+    _check_random(lib, dtype, 512, 384, 256, seed=2)
+
+
+@pytest.mark.parametrize("dtype", ["bfloat16", "float16"])
 @pytest.mark.parametrize("shape", [(2048, 2048, 2048), (1024, 1024, 1024), (640, 1536, 768)])
 def test_few_tiles_take_128x128_tiles(lib, dtype, shape):
     # Several tile rows that would leave half the CUs idle on 128 x 256 tiles
