@@ -4,31 +4,36 @@
 // N % BN == 0 and K a multiple of the stage depth; everything else goes to
 // the generic kernel.
 //
-// Data path. Every stage holds 64 bytes of K per row: A as [BM rows][64 B],
-// B as [K rows][BN * elem bytes] -- B keeps its HBM layout (N-contiguous).
-// Both arrive with buffer_load_dwordx4 ... lds (HBM/L2 -> LDS, no register
+// Data path. A stage is 64 bytes of K per row. A is held two stages at a
+// time, as [BM rows][128 B] pair slots; B one stage at a time, as
+// [K rows][BN * elem bytes] -- B keeps its HBM layout (N-contiguous). Both
+// arrive with buffer_load_dwordx4 ... lds (HBM/L2 -> LDS, no register
 // staging): one wave instruction fills 1 KiB of LDS in lane order, and each
 // lane picks the global 16 bytes that belong at its slot of the swizzled
-// layout. The MFMA operands come out of LDS with ds_read_b128 for A and the
-// gfx950 transposing reads (ds_read_b64_tr_b16 for 16-bit B,
+// layout. An A instruction covers 8 rows x 128 bytes, whole cache lines:
+// loading A one 64-byte stage at a time made two L2 requests per line and
+// ran 2-13% slower. The MFMA operands come out of LDS with ds_read_b128 for
+// A and the gfx950 transposing reads (ds_read_b64_tr_b16 for 16-bit B,
 // ds_read_b64_tr_b8 for fp8 B), which hand each lane 4 (8) consecutive K
 // values of one B column -- the MFMA operand layout -- with no transpose pass
 // anywhere.
 //
 // LDS swizzles (16-byte chunk c of a row is stored at chunk c ^ f(row)):
-//   A rows (4 chunks):          f = ((r >> 1) & 3) ^ ((r >> 3) & 1)
+//   A rows (8 chunks):          f = ((r >> 1) & 7) ^ ((r & 1) << 2)
 //   16-bit B rows (32 chunks):  f = ((k << 2) ^ (k << 1)) & 15, k = row & 3
 //   fp8 B rows (16 chunks):     f = (2k) ^ (k >> 2),            k = row & 7
 // Each keeps every operand read of a wave free of bank conflicts for both 8-
 // and 16-lane LDS phases (checked exhaustively on the host).
 //
-// Pipeline. STAGES LDS slots form a ring with one barrier per stage. While
-// the MFMAs of stage k run from registers, every operand of stage k + 1 is
-// read from LDS into a second register set and the loads of stage
-// k + STAGES go into the slot stage k has just vacated, all spread evenly
-// between the MFMAs; so all STAGES slots have loads in flight. The barrier
-// is a bare s_barrier preceded by an explicit vmcnt wait for the one stage
-// needed next -- a full __syncthreads() would wait for all of them.
+// Pipeline. NA A pair slots and NB B stage slots, one barrier per stage.
+// While the MFMAs of stage k run from registers, every operand of stage
+// k + 1 is read from LDS into a second register set, B stage k + NB is
+// loaded into the slot stage k has just vacated and, on odd k, A pair
+// (k - 1) / 2 + NA into the pair slot whose second stage was k; all spread
+// evenly between the MFMAs. The barrier is a bare s_barrier preceded by an
+// explicit vmcnt wait for the loads of stage k + 1 only, derived at compile
+// time from the issue order (load_schedule) -- a full __syncthreads() would
+// wait for all of them.
 //
 // Waves form a WGM x WGN grid; each wave owns (BM/WGM) x (BN/WGN) of C as
 // 32 x 32 fragments: v_mfma_f32_32x32x16_{bf16,f16} (two per stage), or for
@@ -45,6 +50,7 @@
 
 #include <cmath>
 #include <cstdlib>
+#include <numeric>
 #include <utility>
 
 namespace mb {
@@ -101,11 +107,61 @@ struct Traits<MB_DT_FLOAT8_E5M2> : Traits<MB_DT_FLOAT8_E4M3FN> {
     }
 };
 
-// One 16-byte piece of this lane's A operand: row `row` of the stage, 16-byte
-// K chunk `chunk` (16-bit: chunk 2s + lane/32 of substep s; fp8: chunks
-// 2*(lane/32) and +1 form the 32-byte operand).
-__device__ __forceinline__ u32x4 read_a_piece(const unsigned char* st, int row, int chunk) {
-    return *reinterpret_cast<const u32x4*>(st + row * kStageK + ((chunk ^ swz_a(row)) << 4));
+// A is held two stages at a time: rows of 128 bytes (stage 2p in chunks 0-3,
+// stage 2p + 1 in chunks 4-7), chunk c of row r stored at chunk c ^ swz_a2(r).
+// For the operand reads (32 consecutive rows, one logical chunk per half
+// wave) every 8 consecutive rows land on 8 distinct 16-byte bank groups and
+// every 16 on 16 distinct (row parity, chunk) pairs: no bank conflicts for 8-
+// or 16-lane LDS phases.
+__device__ __forceinline__ int swz_a2(int r) { return ((r >> 1) & 7) ^ ((r & 1) << 2); }
+
+// One 16-byte piece of this lane's A operand: row `row` of the pair slot,
+// 16-byte K chunk `chunk` (0..7: 4 * stage parity + chunk within the stage;
+// 16-bit: chunk 2s + lane/32 of substep s; fp8: chunks 2*(lane/32) and +1
+// form the 32-byte operand).
+__device__ __forceinline__ u32x4 read_a_piece(const unsigned char* slot, int row, int chunk) {
+    return *reinterpret_cast<const u32x4*>(slot + row * 2 * kStageK + ((chunk ^ swz_a2(row)) << 4));
+}
+
+// Issue order of the LDS-DMA loads and the vmcnt waits it allows. Loop step j
+// issues, in this order, the A pair (j - 1) / 2 + NA when j is odd (AI loads
+// per wave) and B stage j + NB (BI loads). The prologue issues A pairs
+// 0..NA-1 and B stages 0..NB-1 in the order the same rule gives for the
+// steps -V..-1 that precede step 0. Before step j the pipeline needs stage
+// j + 1: B stage j + 1 and A pair (j + 1) / 2; wait(j) is the number of loads
+// issued after the later of the two, i.e. the vmcnt at which both have
+// landed. Loads complete in issue order. The loop uses, per step parity, the
+// smallest wait over the first steps and the steady state, so every step's
+// wait is exact or stricter; `prologue` is the wait before stage 0 is read.
+struct LoadSchedule {
+    int odd_wait, even_wait, prologue;
+};
+
+constexpr LoadSchedule load_schedule(int NA, int NB, int AI, int BI) {
+    constexpr int kSteps = 64;
+    // end[kind][index]: loads issued up to and including that pair (kind 0)
+    // or stage (kind 1); issued_before[j]: loads issued before step j.
+    int end_a[2 * kSteps] = {}, end_b[2 * kSteps] = {}, issued_before[kSteps] = {};
+    int total = 0;
+    const int V = 2 * NA - 1 > NB ? 2 * NA - 1 : NB;
+    for (int v = -V; v < kSteps; ++v) {
+        if (v >= 0) issued_before[v] = total;
+        if ((v & 1) != 0) {
+            const int pair = (v - 1 >= 0 ? (v - 1) / 2 : -((1 - v) / 2)) + NA;
+            if (pair >= 0 && pair < 2 * kSteps) end_a[pair] = (total += AI);
+        }
+        if (v + NB >= 0 && v + NB < 2 * kSteps) end_b[v + NB] = (total += BI);
+    }
+    LoadSchedule r{1 << 20, 1 << 20, 0};
+    const int p0 = end_a[0] > end_b[0] ? end_a[0] : end_b[0];
+    r.prologue = issued_before[0] - p0;
+    for (int j = 0; j + 1 < kSteps; ++j) {
+        const int need = end_a[(j + 1) / 2] > end_b[j + 1] ? end_a[(j + 1) / 2] : end_b[j + 1];
+        const int w = issued_before[j] - need;
+        if (j & 1) r.odd_wait = w < r.odd_wait ? w : r.odd_wait;
+        else r.even_wait = w < r.even_wait ? w : r.even_wait;
+    }
+    return r;
 }
 
 // One transposing read of this lane's B operand (column nb + lane % 32).
@@ -145,7 +201,7 @@ __device__ __forceinline__ u32x2 pack4(float a, float b, float c, float d) {
     }
 }
 
-template <int DT, int BM, int BN, int WGM, int WGN, int STAGES, bool SCALED>
+template <int DT, int BM, int BN, int WGM, int WGN, int NA, int NB, bool SCALED>
 __global__ void __launch_bounds__(64 * WGM * WGN)
 gemm_tiled_kernel(const unsigned char* __restrict__ A, const unsigned char* __restrict__ B,
                   unsigned char* __restrict__ C, int M, int N, int K, float alpha, int tiles_m,
@@ -157,32 +213,32 @@ gemm_tiled_kernel(const unsigned char* __restrict__ A, const unsigned char* __re
     constexpr int WTM = BM / WGM, WTN = BN / WGN;
     constexpr int FM = WTM / 32, FN = WTN / 32;
     constexpr int K_ROWS = kStageK / E;                 // K elements per stage = B rows per stage
-    constexpr int A_BYTES = BM * kStageK;
+    constexpr int PAIR = 2 * BM * kStageK;              // A slot: two stages, [BM][128 B]
     constexpr int B_ROW = BN * E;                       // bytes per B row in LDS
-    constexpr int B_BYTES = K_ROWS * B_ROW;
-    constexpr int SLOT = A_BYTES + B_BYTES;
-    constexpr int A_INSTR = A_BYTES / 1024 / W;         // LDS-DMA instructions per wave per stage
-    constexpr int B_INSTR = B_BYTES / 1024 / W;
-    constexpr int LOADS = A_INSTR + B_INSTR;
-    static_assert(A_BYTES % (1024 * W) == 0 && B_BYTES % (1024 * W) == 0, "stage must split over the waves");
+    constexpr int B_BYTES = K_ROWS * B_ROW;             // B slot: one stage
+    constexpr int A_INSTR = PAIR / 1024 / W;            // LDS-DMA instructions per wave per A pair
+    constexpr int B_INSTR = B_BYTES / 1024 / W;         // ... per B stage
+    constexpr int LDS_BYTES = NA * PAIR + NB * B_BYTES;
+    static_assert(PAIR % (1024 * W) == 0 && B_BYTES % (1024 * W) == 0, "stage must split over the waves");
+    static_assert(A_INSTR % 2 == 0, "A offsets assume an even number of pair loads per wave");
     static_assert(B_ROW == 512 || B_ROW == 256, "B swizzle assumes 256- or 512-byte rows");
     static_assert(WTM % 32 == 0 && WTN % 32 == 0, "wave tile must be 32-aligned");
-    static_assert(STAGES >= 4 && STAGES <= 6 && STAGES * SLOT <= 160 * 1024, "LDS ring does not fit");
+    static_assert(NA >= 2 && NB >= 3 && LDS_BYTES <= 160 * 1024, "LDS ring does not fit");
+    constexpr LoadSchedule kSched = load_schedule(NA, NB, A_INSTR, B_INSTR);
+    static_assert(kSched.prologue >= 0 && kSched.odd_wait >= 0 && kSched.even_wait >= 0 &&
+                  kSched.prologue < 64 && kSched.odd_wait < 64 && kSched.even_wait < 64,
+                  "load schedule leaves a needed stage unissued or overflows vmcnt");
 
-    // One array per ring slot, so every slot address is a compile-time choice.
-    __shared__ __attribute__((aligned(1024))) unsigned char ring0[SLOT], ring1[SLOT], ring2[SLOT];
-    __shared__ __attribute__((aligned(1024))) unsigned char ring3[STAGES > 3 ? SLOT : 1024];
-    __shared__ __attribute__((aligned(1024))) unsigned char ring4[STAGES > 4 ? SLOT : 1024];
-    __shared__ __attribute__((aligned(1024))) unsigned char ring5[STAGES > 5 ? SLOT : 1024];
-    auto slot_ptr = [&](auto idx) -> unsigned char* {
-        constexpr int i = decltype(idx)::value;
-        static_assert(i < STAGES, "slot out of range");
-        if constexpr (i == 0) return ring0;
-        else if constexpr (i == 1) return ring1;
-        else if constexpr (i == 2) return ring2;
-        else if constexpr (i == 3) return ring3;
-        else if constexpr (i == 4) return ring4;
-        else return ring5;
+    // One LDS array: NA A pair slots, then NB B stage slots; every slot
+    // address is a compile-time offset.
+    __shared__ __attribute__((aligned(1024))) unsigned char lds[LDS_BYTES];
+    auto a_slot = [&](auto idx) -> unsigned char* {
+        static_assert(decltype(idx)::value < NA, "A slot out of range");
+        return lds + decltype(idx)::value * PAIR;
+    };
+    auto b_slot = [&](auto idx) -> unsigned char* {
+        static_assert(decltype(idx)::value < NB, "B slot out of range");
+        return lds + NA * PAIR + decltype(idx)::value * B_BYTES;
     };
 
     const int tid = threadIdx.x;
@@ -207,14 +263,18 @@ gemm_tiled_kernel(const unsigned char* __restrict__ A, const unsigned char* __re
     const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<unsigned char*>(B) + (int64_t)tn * BN * E, (short)0, K * ldb, kBufferFlags);
 
-    // Global byte offsets of this lane's 16-byte pieces (stage 0); a stage
-    // advances A by kStageK bytes and B by K_ROWS rows.
-    int a_voff[A_INSTR], b_voff[B_INSTR];
+    // Global byte offsets of this lane's 16-byte pieces (pair 0 / stage 0);
+    // a pair advances A by 2 * kStageK bytes, a stage advances B by K_ROWS
+    // rows. A load q of a wave fills rows 8 * (wave * A_INSTR + q) .. +7 with
+    // whole 128-byte lines; the swizzle of those rows depends on q only
+    // through its parity, so two vector offsets serve all q and the rest,
+    // 16 * (q / 2) rows, is a uniform offset.
+    int a_voff[2], b_voff[B_INSTR];
 #pragma unroll
-    for (int q = 0; q < A_INSTR; ++q) {
-        const int lin = (wave * A_INSTR + q) * 1024 + lane * 16;   // LDS byte in the A part
-        const int row = lin / kStageK, pchunk = (lin % kStageK) >> 4;
-        a_voff[q] = row * lda + ((pchunk ^ swz_a(row)) << 4);
+    for (int q = 0; q < 2; ++q) {
+        const int lin = (wave * A_INSTR + q) * 1024 + lane * 16;   // LDS byte in the pair slot
+        const int row = lin / (2 * kStageK), pchunk = (lin % (2 * kStageK)) >> 4;
+        a_voff[q] = row * lda + ((pchunk ^ swz_a2(row)) << 4);
     }
 #pragma unroll
     for (int q = 0; q < B_INSTR; ++q) {
@@ -224,26 +284,17 @@ gemm_tiled_kernel(const unsigned char* __restrict__ A, const unsigned char* __re
         b_voff[q] = row * ldb + ((pchunk ^ f) << 4);
     }
 
-    // DMA instruction q (A pieces first, then B) of stage kt into `slot`.
-    auto issue_one = [&](int kt, unsigned char* slot, auto idx) {
+    // DMA instruction q of A pair `pair` into `slot`, and of B stage `kt`.
+    auto issue_a = [&](int pair, unsigned char* slot, auto idx) {
         constexpr int q = decltype(idx)::value;
         const unsigned base = (unsigned)(uintptr_t)(MB_LDS unsigned char*)slot;
-        if constexpr (q < A_INSTR) {
-            lds_dma16(ra, base + (wave * A_INSTR + q) * 1024, a_voff[q], k0 * E + kt * kStageK);
-        } else {
-            constexpr int qb = q - A_INSTR;
-            lds_dma16(rb, base + A_BYTES + (wave * B_INSTR + qb) * 1024, b_voff[qb], (k0 + kt * K_ROWS) * ldb);
-        }
+        lds_dma16(ra, base + (wave * A_INSTR + q) * 1024, a_voff[q & 1],
+                  k0 * E + pair * 2 * kStageK + 16 * (q >> 1) * lda);
     };
-    auto issue_stage = [&](int kt, unsigned char* slot) {
+    auto issue_b = [&](int kt, unsigned char* slot, auto idx) {
+        constexpr int q = decltype(idx)::value;
         const unsigned base = (unsigned)(uintptr_t)(MB_LDS unsigned char*)slot;
-        const int a_soff = k0 * E + kt * kStageK;
-#pragma unroll
-        for (int q = 0; q < A_INSTR; ++q) lds_dma16(ra, base + (wave * A_INSTR + q) * 1024, a_voff[q], a_soff);
-        const int b_soff = (k0 + kt * K_ROWS) * ldb;
-#pragma unroll
-        for (int q = 0; q < B_INSTR; ++q)
-            lds_dma16(rb, base + A_BYTES + (wave * B_INSTR + q) * 1024, b_voff[q], b_soff);
+        lds_dma16(rb, base + (wave * B_INSTR + q) * 1024, b_voff[q], (k0 + kt * K_ROWS) * ldb);
     };
 
     f32x16 acc[FM][FN];
@@ -269,13 +320,6 @@ gemm_tiled_kernel(const unsigned char* __restrict__ A, const unsigned char* __re
     constexpr int PER_SUB = FM * A_PIECES + FN * B_PIECES;
     constexpr int N_READS = SUBS * PER_SUB;
     constexpr int N_MFMA = SUBS * FM * FN;
-    constexpr int N_MEM = N_READS + LOADS;              // memory instructions per step
-    constexpr int PER = (N_MEM + N_MFMA - 1) / N_MFMA;  // ... issued after each MFMA
-    // Memory instruction m of a step is a load when m + 1 is one of the first
-    // LOADS multiples of kLoadStride, otherwise the next operand read: the
-    // loads sit evenly among the reads.
-    constexpr int kLoadStride = N_MEM / LOADS;
-    constexpr auto kIsLoad = [](int m) { return (m + 1) % kLoadStride == 0 && (m + 1) / kLoadStride <= LOADS; };
     struct StageOps {
         Frag a[SUBS][FM];
         Frag b[SUBS][FN];
@@ -283,19 +327,21 @@ gemm_tiled_kernel(const unsigned char* __restrict__ A, const unsigned char* __re
 
     // Read number r of a stage, in the order the MFMAs consume operands: per
     // substep A fragment 0, then the B fragments, then A fragments 1..FM-1.
-    auto read_op = [&](const unsigned char* slot, auto idx, StageOps& o) {
+    // `aslot` is the stage's A pair slot and P its half (the stage's parity).
+    auto read_op = [&](const unsigned char* aslot, const unsigned char* bslot, auto par, auto idx, StageOps& o) {
+        constexpr int P = decltype(par)::value;
         constexpr int r = decltype(idx)::value;
         constexpr int s = r / PER_SUB, u = r % PER_SUB;
         if constexpr (u >= A_PIECES && u < A_PIECES + FN * B_PIECES) {
             constexpr int j = (u - A_PIECES) / B_PIECES, t = (u - A_PIECES) % B_PIECES;
-            const u32x2 v = read_b_piece<DT, BN>(slot + A_BYTES, b_col + 32 * j, s, t, lane);
+            const u32x2 v = read_b_piece<DT, BN>(bslot, b_col + 32 * j, s, t, lane);
             o.b[s][j][2 * t] = v[0];
             o.b[s][j][2 * t + 1] = v[1];
         } else {
             constexpr int q = u < A_PIECES ? u : u - FN * B_PIECES;
             constexpr int i = q / A_PIECES, e = q % A_PIECES;
-            const int chunk = kWide ? 2 * half + e : 2 * s + half;
-            const u32x4 v = read_a_piece(slot, a_row + 32 * i, chunk);
+            const int chunk = 4 * P + (kWide ? 2 * half + e : 2 * s + half);
+            const u32x4 v = read_a_piece(aslot, a_row + 32 * i, chunk);
 #pragma unroll
             for (int w = 0; w < 4; ++w) o.a[s][i][4 * e + w] = v[w];
         }
@@ -306,43 +352,76 @@ gemm_tiled_kernel(const unsigned char* __restrict__ A, const unsigned char* __re
         acc[i][j] = Tr::mfma(o.b[s][j], o.a[s][i], acc[i][j]);
     };
 
-    // Software pipeline over a ring of STAGES slots, one barrier per stage:
-    //   step kt (stage kt in slot kt % STAGES, its operands already in
-    //   registers):
-    //     wait for this wave's loads of stage kt+1 and its LDS reads, barrier
-    //     the stage's MFMAs, with the LDS reads of all of stage kt+1 (into the
-    //     other register set) and the loads of stage kt+STAGES (into slot kt)
-    //     spread evenly between them
-    // The barrier certifies stage kt+1 for every wave, and that every wave has
-    // finished reading slot kt (those reads went out during step kt-1), so all
-    // STAGES slots hold loads in flight. Loads past the last stage re-read the
-    // last stage (in bounds, never consumed), so every step issues the same
-    // number of loads and the vmcnt bookkeeping stays uniform.
+    // Software pipeline, one barrier per stage. A sits in NA pair slots (two
+    // stages each, loaded as whole 128-byte lines of every row), B in NB stage
+    // slots. Step kt (stage kt's operands already in registers):
+    //   wait until stage kt+1 has landed and this wave's LDS reads are done,
+    //   barrier; then the stage's MFMAs, with every LDS read of stage kt+1
+    //   (into the other register set) and this step's loads spread evenly
+    //   between them: B stage kt+NB into the B slot stage kt vacated, and, on
+    //   odd steps, A pair (kt-1)/2+NA into the pair slot whose second stage
+    //   (kt) has just been read.
+    // The barrier certifies stage kt+1 for every wave, and that every wave
+    // has finished reading stage kt (those reads went out during step kt-1).
+    // Loads past the last stage (pair) re-read the last one (in bounds, never
+    // consumed), so every step issues a fixed number of loads and the vmcnt
+    // waits (load_schedule) hold at the tail too.
     // sched_barrier(0) after each MFMA and its memory instructions pins the
     // interleaving, so the MFMA pipe never waits behind a burst of issues.
     const int ksteps = k_len / K_ROWS;
     const int last = ksteps - 1;
-    [&]<int... P>(std::integer_sequence<int, P...>) {
-        (issue_stage(min(P, last), slot_ptr(std::integral_constant<int, P>{})), ...);
-    }(std::make_integer_sequence<int, STAGES>{});
+    const int last_pair = last / 2;
+    constexpr int V = 2 * NA - 1 > NB ? 2 * NA - 1 : NB;
+    [&]<int... U>(std::integer_sequence<int, U...>) {
+        ([&] {
+            constexpr int v = U - V;
+            if constexpr ((v & 1) != 0 && (v - 1) / 2 + NA >= 0) {
+                constexpr int pair = (v - 1) / 2 + NA;  // v - 1 is even: exact
+                [&]<int... Q>(std::integer_sequence<int, Q...>) {
+                    (issue_a(min(pair, last_pair), a_slot(std::integral_constant<int, pair>{}),
+                             std::integral_constant<int, Q>{}), ...);
+                }(std::make_integer_sequence<int, A_INSTR>{});
+            }
+            if constexpr (v + NB >= 0) {
+                [&]<int... Q>(std::integer_sequence<int, Q...>) {
+                    (issue_b(min(v + NB, last), b_slot(std::integral_constant<int, v + NB>{}),
+                             std::integral_constant<int, Q>{}), ...);
+                }(std::make_integer_sequence<int, B_INSTR>{});
+            }
+        }(), ...);
+    }(std::make_integer_sequence<int, V>{});
     // Two operand sets, used alternately (step I computes from set I % 2 and
-    // reads into the other); the loop is unrolled to an even number of steps
-    // that is also a multiple of STAGES, so every slot is a compile-time
-    // choice and the sets are never copied.
+    // reads into the other); the loop is unrolled to a multiple of 2 * NA and
+    // of NB steps, so every slot is a compile-time choice and the sets are
+    // never copied.
     StageOps ops[2];
-    wait_vmcnt_and_barrier<LOADS * (STAGES - 1)>();
+    wait_vmcnt_and_barrier<kSched.prologue>();
     [&]<int... R>(std::integer_sequence<int, R...>) {
-        (read_op(slot_ptr(std::integral_constant<int, 0>{}), std::integral_constant<int, R>{}, ops[0]), ...);
+        (read_op(a_slot(std::integral_constant<int, 0>{}), b_slot(std::integral_constant<int, 0>{}),
+                 std::integral_constant<int, 0>{}, std::integral_constant<int, R>{}, ops[0]), ...);
     }(std::make_integer_sequence<int, N_READS>{});
 
     auto step = [&](auto idx, int kt) {
         constexpr int I = decltype(idx)::value;
-        const unsigned char* next_slot = slot_ptr(std::integral_constant<int, (I + 1) % STAGES>{});
-        unsigned char* load_slot = slot_ptr(std::integral_constant<int, I % STAGES>{});
+        constexpr bool ODD = (I & 1) != 0;
+        constexpr int A_LOADS = ODD ? A_INSTR : 0;
+        constexpr int LOADS = A_LOADS + B_INSTR;
+        constexpr int N_MEM = N_READS + LOADS;              // memory instructions this step
+        constexpr int PER = (N_MEM + N_MFMA - 1) / N_MFMA;  // ... issued after each MFMA
+        // Memory instruction m is a load when m + 1 is one of the first LOADS
+        // multiples of kStride, otherwise the next operand read: the loads
+        // sit evenly among the reads (A pair loads first, then B).
+        constexpr int kStride = N_MEM / LOADS;
+        constexpr auto kIsLoad = [](int m) { return (m + 1) % kStride == 0 && (m + 1) / kStride <= LOADS; };
+        const unsigned char* next_a = a_slot(std::integral_constant<int, ((I + 1) / 2) % NA>{});
+        const unsigned char* next_b = b_slot(std::integral_constant<int, (I + 1) % NB>{});
+        unsigned char* load_a = a_slot(std::integral_constant<int, ((I + 2 * NA - 1) / 2) % NA>{});
+        unsigned char* load_b = b_slot(std::integral_constant<int, I % NB>{});
         const StageOps& cur = ops[I % 2];
         StageOps& nxt = ops[(I + 1) % 2];
-        wait_vmcnt_and_barrier<LOADS * (STAGES - 2)>();
-        const int kload = min(kt + STAGES, last);
+        wait_vmcnt_and_barrier<ODD ? kSched.odd_wait : kSched.even_wait>();
+        const int bload = min(kt + NB, last);
+        const int aload = min((kt - 1) / 2 + NA, last_pair);
         [&]<int... Q>(std::integer_sequence<int, Q...>) {
             ([&] {
                 mfma_op(std::integral_constant<int, Q>{}, cur);
@@ -352,10 +431,15 @@ gemm_tiled_kernel(const unsigned char* __restrict__ A, const unsigned char* __re
                     ([&] {
                         constexpr int m = lo + R;
                         if constexpr (kIsLoad(m)) {
-                            issue_one(kload, load_slot, std::integral_constant<int, (m + 1) / kLoadStride - 1>{});
+                            constexpr int l = (m + 1) / kStride - 1;
+                            if constexpr (l < A_LOADS)
+                                issue_a(aload, load_a, std::integral_constant<int, l>{});
+                            else
+                                issue_b(bload, load_b, std::integral_constant<int, l - A_LOADS>{});
                         } else {
-                            constexpr int loads_before = m / kLoadStride < LOADS ? m / kLoadStride : LOADS;
-                            read_op(next_slot, std::integral_constant<int, m - loads_before>{}, nxt);
+                            constexpr int loads_before = m / kStride < LOADS ? m / kStride : LOADS;
+                            read_op(next_a, next_b, std::integral_constant<int, (I + 1) & 1>{},
+                                    std::integral_constant<int, m - loads_before>{}, nxt);
                         }
                     }(), ...);
                 }(std::make_integer_sequence<int, hi - lo>{});
@@ -363,7 +447,7 @@ gemm_tiled_kernel(const unsigned char* __restrict__ A, const unsigned char* __re
             }(), ...);
         }(std::make_integer_sequence<int, N_MFMA>{});
     };
-    constexpr int UNROLL = STAGES % 2 ? 2 * STAGES : STAGES;
+    constexpr int UNROLL = std::lcm(2 * NA, NB);
     for (int kt = 0; kt < ksteps; kt += UNROLL) {
         [&]<int... I>(std::integer_sequence<int, I...>) {
             ((kt + I < ksteps ? step(std::integral_constant<int, I>{}, kt + I) : void()), ...);
@@ -390,11 +474,8 @@ gemm_tiled_kernel(const unsigned char* __restrict__ A, const unsigned char* __re
         constexpr int ROW_BYTES = WTN * 2;
         constexpr int ROW_CHUNKS = ROW_BYTES / 16;
         static_assert(ROW_CHUNKS == 16, "staging swizzle assumes 256-byte rows");
-        static_assert(WTM * ROW_BYTES <= SLOT && W <= STAGES, "a wave's tile must fit its slot");
-        unsigned char* stage = wave == 0   ? slot_ptr(std::integral_constant<int, 0>{})
-                               : wave == 1 ? slot_ptr(std::integral_constant<int, 1>{})
-                               : wave == 2 ? slot_ptr(std::integral_constant<int, 2>{})
-                                           : slot_ptr(std::integral_constant<int, 3>{});
+        static_assert(W * WTM * ROW_BYTES <= LDS_BYTES, "the waves' tiles must fit the LDS ring");
+        unsigned char* stage = lds + wave * WTM * ROW_BYTES;
         // alpha is 1 except for scaled fp8: the unscaled instantiation skips
         // the multiply, a VALU op per accumulator.
         auto stage_tile = [&](auto scaled) {
@@ -488,13 +569,13 @@ gemm_splitk_reduce_kernel(const float* __restrict__ ws, unsigned char* __restric
 }
 
 struct TiledConfig {
-    int bm, bn, wgm, wgn, stages, group_m;
+    int bm, bn, wgm, wgn, na, nb, group_m;  // na A pair slots, nb B stage slots
 };
 
 constexpr TiledConfig kConfigs[] = {
-    {256, 256, 2, 2, 5, 4},  // 0: large problems, 128 x 128 per wave, 5 x 32 KiB stages
-    {128, 256, 2, 2, 6, 8},  // 1: mid-size problems, 64 x 128 per wave, 6 x 24 KiB stages
-    {128, 128, 4, 1, 6, 4},  // 2: 16-bit only, few tiles: 32 x 128 per wave, 6 x 16 KiB stages
+    {256, 256, 2, 2, 3, 4, 4},  // 0: large problems, 128 x 128 per wave; 3 x 32 + 4 x 16 KiB
+    {128, 256, 2, 2, 3, 6, 8},  // 1: mid-size problems, 64 x 128 per wave; 3 x 16 + 6 x 16 KiB
+    {128, 128, 4, 1, 3, 6, 4},  // 2: 16-bit only, few tiles: 32 x 128 per wave; 3 x 16 + 6 x 8 KiB
 };
 constexpr int kNumConfigs = sizeof(kConfigs) / sizeof(kConfigs[0]);
 
@@ -511,11 +592,11 @@ int launch_cfg(const void* A, const void* B, void* C, int64_t M, int64_t N, int6
     auto* cp = static_cast<unsigned char*>(C);
     // Only fp8 carries a scale; the split-K partials are scaled by the reduction.
     if (is_fp8(DT) && alpha != 1.0f && splits == 1) {
-        hipLaunchKernelGGL((gemm_tiled_kernel<DT, c.bm, c.bn, c.wgm, c.wgn, c.stages, is_fp8(DT)>), grid, block, 0,
+        hipLaunchKernelGGL((gemm_tiled_kernel<DT, c.bm, c.bn, c.wgm, c.wgn, c.na, c.nb, is_fp8(DT)>), grid, block, 0,
                            stream, a, b, cp, (int)M, (int)N, (int)K, alpha, tiles_m, tiles_n, c.group_m, splits,
                            (int)(K / splits), ws);
     } else {
-        hipLaunchKernelGGL((gemm_tiled_kernel<DT, c.bm, c.bn, c.wgm, c.wgn, c.stages, false>), grid, block, 0,
+        hipLaunchKernelGGL((gemm_tiled_kernel<DT, c.bm, c.bn, c.wgm, c.wgn, c.na, c.nb, false>), grid, block, 0,
                            stream, a, b, cp, (int)M, (int)N, (int)K, 1.0f, tiles_m, tiles_n, c.group_m, splits,
                            (int)(K / splits), ws);
     }
@@ -628,7 +709,7 @@ int gemm_tiled_plan(int dtype, int64_t M, int64_t N, int64_t K, const DeviceProp
     plan->frag_m = 32;
     plan->frag_n = 32;
     plan->frag_k = is_fp8(dtype) ? 64 : 16;
-    plan->k_stages = c.stages;
+    plan->k_stages = c.nb;
     plan->split_k = splits;
     plan->tile_group_m = c.group_m;
     plan->workspace = splits > 1 ? (size_t)splits * (size_t)M * (size_t)N * sizeof(float) : 0;
