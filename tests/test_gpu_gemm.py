@@ -86,6 +86,38 @@ def test_tiled_configurations(lib, dtype, config, shape, monkeypatch):
     _check_random(lib, dtype, m, n, k, seed=k)
 
 
+@pytest.mark.parametrize("dtype", ["bfloat16", "float8_e4m3fn"])
+@pytest.mark.parametrize("config", ["0", "1", "2"])
+@pytest.mark.parametrize("ksteps", [1, 2, 3, 4, 5, 6, 7, 8, 9, 11, 12, 13, 25, 37])
+def test_tiled_stage_counts(lib, dtype, config, ksteps, monkeypatch):
+    # A is loaded two 64-byte K stages at a time: odd stage counts leave the
+    # last pair half used, and counts around the 12-step unroll exercise the
+    # tail loads that re-read the last stage / pair.
+    if config == "2" and dtype.startswith("float8"):
+        pytest.skip("128 x 128 tiles take 16-bit inputs only")
+    monkeypatch.setenv("MB_GEMM_TILED_CONFIG", config)
+    monkeypatch.setenv("MB_GEMM_SPLITS", "1")  # the 128-row tiles would split K for this few tiles
+    k = ksteps * (64 if dtype.startswith("float8") else 32)
+    m, n = 300, 512
+    info = lib.gemm_info(capi.DTYPES[dtype], m, n, k)
+    assert info["implementation"] == "gfx950_mfma32_lds_dma" and info["split_k"] == 1
+    print(f"[gemm] stages {ksteps} cfg {config} {dtype} {m}x{n}x{k}", flush=True)
+    _check_random(lib, dtype, m, n, k, seed=ksteps)
+
+
+@pytest.mark.parametrize("dtype", ["bfloat16", "float8_e4m3fn"])
+@pytest.mark.parametrize("splits, ksteps", [(3, 15), (3, 21), (5, 35), (7, 7)])
+def test_forced_splits_with_odd_stage_counts(lib, dtype, splits, ksteps, monkeypatch):
+    # Each split runs ksteps / splits stages (odd here), writing fp32 partials.
+    monkeypatch.setenv("MB_GEMM_SPLITS", str(splits))
+    k = ksteps * (64 if dtype.startswith("float8") else 32)
+    m, n = 128, 512
+    info = lib.gemm_info(capi.DTYPES[dtype], m, n, k)
+    assert info["implementation"] == "gfx950_mfma32_lds_dma" and info["split_k"] == splits
+    print(f"[gemm] splits {splits} x {ksteps // splits} stages {dtype} {m}x{n}x{k}", flush=True)
+    _check_random(lib, dtype, m, n, k, seed=splits)
+
+
 @pytest.mark.parametrize("dtype", ["bfloat16", "float16"])
 @pytest.mark.parametrize("shape", [(512, 384, 256), (1000, 1152, 320), (64, 640, 512), (16, 1152, 4096), (3, 128, 64)])
 def test_n_multiple_of_128_takes_128x128_tiles(lib, dtype, shape, monkeypatch):
