@@ -665,30 +665,41 @@ int gemm_tiled_plan(int dtype, int64_t M, int64_t N, int64_t K, const DeviceProp
     //   partials (s > 1): the fp32 partials written and read back,
     //            2 * s * M * N * 4 bytes at ~5 TB/s, plus ~5 us for the
     //            reduction's launch.
-    // time(s) = max(MFMA, stream) + partials; the smallest time wins.
+    // time(s) = max(MFMA, stream) + partials; the smallest time wins. For
+    // 16-bit inputs the model rates both 128-row configurations, 128 x 256
+    // and 128 x 128 tiles (twice the blocks for the same B traffic: skinny
+    // and few-tile shapes fill the CUs with fewer K splits), keeping 128 x 256
+    // on a tie. Against the previous choice of 128 x 256 tiles alone it ran
+    // every shape it changes faster on MI355X, bf16: 16..256 x 8192 x 8192
+    // by 2-7%, 128 x 4096 x 4096 by 21%, 256 x 512 x 1024 by 34%.
     int splits = 1;
     if (kConfigs[cfg].bm == 128) {
-        const double bm = kConfigs[cfg].bm, bn = kConfigs[cfg].bn;
+        const int cands[2] = {cfg, 2};
+        const int n_cands = (!forced && cfg == 1 && e == 2) ? 2 : 1;
         const double flops_per_cu = 6.0e12 * (e == 1 ? 2.0 : 1.0), bw = 5.0e12;
-        double best = 0.0;
-        for (int64_t s = 1; s <= 32; s *= 2) {
-            if (K % (stage_k * s) != 0) continue;
-            const double rounds = (double)((tiles(cfg) * s + cus - 1) / cus);
-            const double mfma = rounds * 2.0 * bm * bn * ((double)K / (double)s) / flops_per_cu;
-            const double rows_in_flight = (double)(s * N * e) / 65536.0;
-            const double stream = (double)((K * N + M * K) * e) / bw * std::sqrt(rows_in_flight > 1.0 ? rows_in_flight : 1.0);
-            const double partials = s > 1 ? 2.0 * (double)s * (double)M * (double)N * 4.0 / bw + 5.0e-6 : 0.0;
-            const double t = (mfma > stream ? mfma : stream) + partials;
-            if (s == 1 || t < best) {
-                best = t;
-                splits = (int)s;
+        double best = -1.0;
+        int best_cfg = cfg;
+        for (int ci = 0; ci < n_cands; ++ci) {
+            const int c = cands[ci];
+            const double bm = kConfigs[c].bm, bn = kConfigs[c].bn;
+            for (int64_t s = 1; s <= 32; s *= 2) {
+                if (K % (stage_k * s) != 0) continue;
+                const double rounds = (double)((tiles(c) * s + cus - 1) / cus);
+                const double mfma = rounds * 2.0 * bm * bn * ((double)K / (double)s) / flops_per_cu;
+                const double rows_in_flight = (double)(s * N * e) / 65536.0;
+                const double stream =
+                    (double)((K * N + M * K) * e) / bw * std::sqrt(rows_in_flight > 1.0 ? rows_in_flight : 1.0);
+                const double partials = s > 1 ? 2.0 * (double)s * (double)M * (double)N * 4.0 / bw + 5.0e-6 : 0.0;
+                const double t = (mfma > stream ? mfma : stream) + partials;
+                if (best < 0.0 || t < best) {
+                    best = t;
+                    best_cfg = c;
+                    splits = (int)s;
+                }
             }
         }
+        cfg = best_cfg;
     }
-    // Several tile rows, no split and at most half the CUs busy (2048^3 makes
-    // 128 tiles of 128 x 256): 16-bit inputs take 128 x 128 tiles instead,
-    // twice the blocks for the same B panel traffic per tile row.
-    if (!forced && cfg == 1 && splits == 1 && e == 2 && M > kConfigs[1].bm && tiles(1) * 2 <= cus) cfg = 2;
     const char* force_splits = std::getenv("MB_GEMM_SPLITS");  // tuning/testing override
     if (force_splits != nullptr && *force_splits != '\0') {
         const int f = std::atoi(force_splits);

@@ -152,13 +152,22 @@ def test_few_tiles_take_128x128_tiles(lib, dtype, shape):
 
 @pytest.mark.parametrize("dtype", ["bfloat16", "float16"])
 @pytest.mark.parametrize("shape", [(16, 8192, 8192), (128, 8192, 8192)])
-def test_skinny_benchmark_shapes_split_four_ways(lib, dtype, shape):
-    # The split-K cost model's pick for the two skinny benchmark shapes: 4 splits over 128-row tiles
-    # (measured 26 / 34 us; 16 / 8 splits, the count a tile-count rule picks, ran 31 / 45 us).
+def test_skinny_benchmark_shapes_split_two_ways_on_128x128_tiles(lib, dtype, shape):
+    # The split-K cost model's pick for the two skinny benchmark shapes with 16-bit inputs: 2 splits over
+    # 128 x 128 tiles (measured 24.7 / 31.4 us against 25.9 / 32.2 for 4 splits over 128 x 256 tiles, and
+    # 31 / 45 us for the 16 / 8 splits a tile-count rule picks).
     m, n, k = shape
     info = lib.gemm_info(capi.DTYPES[dtype], m, n, k)
+    assert (info["tile_m"], info["tile_n"], info["split_k"]) == (128, 128, 2)
+    assert lib.gemm_workspace_size(capi.DTYPES[dtype], m, n, k) == 2 * m * n * 4
+    _check_random(lib, dtype, m, n, k, seed=m, rows=64)
+
+
+@pytest.mark.parametrize("dtype", ["float8_e4m3fn", "float8_e5m2"])
+def test_fp8_skinny_keeps_128x256_tiles(lib, dtype):
+    # fp8 has no 128 x 128 configuration: the model rates 128 x 256 tiles only.
+    info = lib.gemm_info(capi.DTYPES[dtype], 128, 8192, 8192)
     assert (info["tile_m"], info["tile_n"], info["split_k"]) == (128, 256, 4)
-    assert lib.gemm_workspace_size(capi.DTYPES[dtype], m, n, k) == 4 * m * n * 4
 
 
 @pytest.mark.parametrize("dtype", LOWP)
