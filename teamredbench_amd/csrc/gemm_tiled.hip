@@ -1,8 +1,8 @@
 // LDS-pipelined MFMA GEMM for gfx950: C = alpha * (A * B), A (M x K) and
 // B (K x N) row-major, fp32 accumulation, output bf16 (bf16 and fp8 e4m3 /
-// e5m2 inputs) or fp16 (fp16 inputs). Takes shapes with M % BM == 0,
-// N % BN == 0 and K a multiple of the stage depth; everything else goes to
-// the generic kernel.
+// e5m2 inputs) or fp16 (fp16 inputs). Takes shapes with N % BN == 0 and K a
+// multiple of the stage depth, any M (the rows of a partial last M tile read
+// as zeros and are not stored); everything else goes to the generic kernel.
 //
 // Data path. A stage is 64 bytes of K per row. A is held two stages at a
 // time, as [BM rows][128 B] pair slots; B one stage at a time, as
@@ -459,8 +459,8 @@ gemm_tiled_kernel(const unsigned char* __restrict__ A, const unsigned char* __re
     // C[row = 32*i + l % 32][col = 32*j + 8g + 4*(l / 32) + q]: stored straight
     // from registers, every store instruction would put 16 bytes into each of
     // 32 rows. Instead each wave rounds its (WTM x WTN) tile to 16 bits into
-    // the LDS slot with its own index (every slot is free after the final
-    // barrier), then reads it back row by row so that 16 lanes store one
+    // its own region of the LDS ring (all of it is free after the final wait
+    // and barrier), then reads it back row by row so that 16 lanes store one
     // 256-byte row segment: whole cache lines, half the store instructions.
     // Staged rows are 16 chunks of 16 bytes; chunk c of row r sits at chunk
     // c ^ (r % 16), which keeps both the writes (32 rows, one chunk) and the
