@@ -71,7 +71,6 @@ struct Traits;
 template <>
 struct Traits<MB_DT_BFLOAT16> {
     static constexpr int kElem = 2;
-    static constexpr int kSub = 2;          // MFMAs per fragment pair per stage (K = 16 each)
     typedef u32x4 Frag;
     __device__ static __forceinline__ f32x16 mfma(const Frag& a, const Frag& b, f32x16 c) {
         return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
@@ -90,7 +89,6 @@ struct Traits<MB_DT_FLOAT16> : Traits<MB_DT_BFLOAT16> {
 template <>
 struct Traits<MB_DT_FLOAT8_E4M3FN> {
     static constexpr int kElem = 1;
-    static constexpr int kSub = 1;          // one 32x32x64 MFMA per fragment pair per stage
     typedef i32x8 Frag;
     // Format code 0 = e4m3 for both operands; zero scale operands select the
     // unscaled encoding of the instruction.
