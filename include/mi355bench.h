@@ -106,7 +106,7 @@ int mb_time_stream(int op, int dtype, void* dst, const void* b, const void* c,
  * scale_a/scale_b are the fp8 per-tensor dequantisation scales (ignored for
  * the other types). Leading dimensions are K, N and N. Any M, N, K >= 1 with
  * 16-byte aligned base pointers; shapes the pipelined kernels do not divide
- * (16-bit: N % 128, fp8: N % 256; K % 64 bytes) run on bounds-checked kernels.
+ * (N % 128, K % 64 bytes) run on bounds-checked kernels.
  * FLOAT32 / FLOAT64 follow the reference's high-precision path
  * (mfu_gemm_highp.hip.hpp:39-218) on v_mfma_f32_32x32x2_f32 and
  * v_mfma_f64_16x16x4_f64; FLOAT8_E5M2 is the dtype the reference declares

@@ -22,6 +22,7 @@
 //   A rows (8 chunks):          f = ((r >> 1) & 7) ^ ((r & 1) << 2)
 //   16-bit B rows (32 chunks):  f = ((k << 2) ^ (k << 1)) & 15, k = row & 3
 //   fp8 B rows (16 chunks):     f = (2k) ^ (k >> 2),            k = row & 7
+//   fp8 B rows (8 chunks):      f = k,                          k = row & 7
 // Each keeps every operand read of a wave free of bank conflicts for both 8-
 // and 16-lane LDS phases (checked exhaustively on the host).
 //
@@ -59,7 +60,9 @@ namespace {
 constexpr int kStageK = 64;                  // bytes of K per row per stage
 
 __device__ __forceinline__ int swz_b16(int k) { return ((k << 2) ^ (k << 1)) & 15; }
+// fp8 B rows of 256 bytes (256 columns) and of 128 bytes (128 columns).
 __device__ __forceinline__ int swz_b8(int k) { return (2 * k) ^ (k >> 2); }
+__device__ __forceinline__ int swz_b8_128(int k) { return k; }
 
 typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x4_t __attribute__((__vector_size__(4 * sizeof(__bf16))));
@@ -181,7 +184,8 @@ __device__ __forceinline__ u32x2 read_b_piece(const unsigned char* st, int nb, i
         constexpr int row_bytes = BN;
         const int k = 32 * (g >> 1) + 8 * t + (i >> 1);
         const int n = nb + 16 * (g & 1) + 8 * (i & 1);
-        const int off = k * row_bytes + (((n >> 4) ^ swz_b8(k & 7)) << 4) + 8 * (i & 1);
+        const int f = row_bytes == 256 ? swz_b8(k & 7) : swz_b8_128(k & 7);
+        const int off = k * row_bytes + (((n >> 4) ^ f) << 4) + 8 * (i & 1);
         const i32x2_t v = __builtin_amdgcn_ds_read_tr8_b64_v2i32((MB_LDS i32x2_t*)((MB_LDS unsigned char*)st + off));
         return __builtin_bit_cast(u32x2, v);
     }
@@ -219,7 +223,8 @@ gemm_tiled_kernel(const unsigned char* __restrict__ A, const unsigned char* __re
     constexpr int LDS_BYTES = NA * PAIR + NB * B_BYTES;
     static_assert(PAIR % (1024 * W) == 0 && B_BYTES % (1024 * W) == 0, "stage must split over the waves");
     static_assert(A_INSTR % 2 == 0, "A offsets assume an even number of pair loads per wave");
-    static_assert(B_ROW == 512 || B_ROW == 256, "B swizzle assumes 256- or 512-byte rows");
+    static_assert(B_ROW == 512 || B_ROW == 256 || (E == 1 && B_ROW == 128),
+                  "B swizzles cover 16-bit rows of 512 / 256 bytes and fp8 rows of 256 / 128 bytes");
     static_assert(WTM % 32 == 0 && WTN % 32 == 0, "wave tile must be 32-aligned");
     static_assert(NA >= 2 && NB >= 3 && LDS_BYTES <= 160 * 1024, "LDS ring does not fit");
     constexpr LoadSchedule kSched = load_schedule(NA, NB, A_INSTR, B_INSTR);
@@ -278,7 +283,7 @@ gemm_tiled_kernel(const unsigned char* __restrict__ A, const unsigned char* __re
     for (int q = 0; q < B_INSTR; ++q) {
         const int lin = (wave * B_INSTR + q) * 1024 + lane * 16;   // LDS byte in the B part
         const int row = lin / B_ROW, pchunk = (lin % B_ROW) >> 4;
-        const int f = E == 2 ? swz_b16(row & 3) : swz_b8(row & 7);
+        const int f = E == 2 ? swz_b16(row & 3) : B_ROW == 256 ? swz_b8(row & 7) : swz_b8_128(row & 7);
         b_voff[q] = row * ldb + ((pchunk ^ f) << 4);
     }
 
@@ -573,7 +578,7 @@ struct TiledConfig {
 constexpr TiledConfig kConfigs[] = {
     {256, 256, 2, 2, 3, 4, 4},  // 0: large problems, 128 x 128 per wave; 3 x 32 + 4 x 16 KiB
     {128, 256, 2, 2, 3, 6, 8},  // 1: mid-size problems, 64 x 128 per wave; 3 x 16 + 6 x 16 KiB
-    {128, 128, 4, 1, 3, 6, 4},  // 2: 16-bit only, few tiles: 32 x 128 per wave; 3 x 16 + 6 x 8 KiB
+    {128, 128, 4, 1, 3, 6, 4},  // 2: few tiles, N % 256 != 0: 32 x 128 per wave; 3 x 16 + 6 x 8 KiB
 };
 constexpr int kNumConfigs = sizeof(kConfigs) / sizeof(kConfigs[0]);
 
@@ -613,11 +618,7 @@ template <int DT>
 int launch_dtype(const GemmPlan& plan, const void* A, const void* B, void* C, int64_t M, int64_t N, int64_t K,
                  float alpha, void* workspace, hipStream_t stream) {
     if (plan.config == 0) return launch_cfg<DT, 0>(A, B, C, M, N, K, alpha, plan, workspace, stream);
-    // 128-column tiles have 256-byte B rows for 16-bit inputs only (the fp8
-    // B swizzle assumes 256-byte rows of 256 columns).
-    if constexpr (!is_fp8(DT)) {
-        if (plan.config == 2) return launch_cfg<DT, 2>(A, B, C, M, N, K, alpha, plan, workspace, stream);
-    }
+    if (plan.config == 2) return launch_cfg<DT, 2>(A, B, C, M, N, K, alpha, plan, workspace, stream);
     return launch_cfg<DT, 1>(A, B, C, M, N, K, alpha, plan, workspace, stream);
 }
 
@@ -630,10 +631,9 @@ int gemm_tiled_plan(int dtype, int64_t M, int64_t N, int64_t K, const DeviceProp
                     GemmPlan* plan) {
     const int64_t e = is_fp8(dtype) ? 1 : 2;
     const int64_t stage_k = kStageK / e;
-    // N in 256-column tiles, or for 16-bit inputs in 128-column tiles
-    // (configuration 2; its B rows are 256 bytes, the 16-bit swizzle's width).
+    // N in 256-column tiles, or in 128-column tiles (configuration 2).
     const bool n128_only = N % 256 != 0;
-    if (K % stage_k != 0 || N % 128 != 0 || (n128_only && e != 2)) return MB_ERR_SHAPE;
+    if (K % stage_k != 0 || N % 128 != 0) return MB_ERR_SHAPE;
     if (K * N * e >= (int64_t(1) << 31) || 256 * K * e >= (int64_t(1) << 31) || M >= (int64_t(1) << 31) ||
         M * N >= (int64_t(1) << 31))
         return MB_ERR_SHAPE;
@@ -643,7 +643,7 @@ int gemm_tiled_plan(int dtype, int64_t M, int64_t N, int64_t K, const DeviceProp
     const char* force = std::getenv("MB_GEMM_TILED_CONFIG");  // tuning/testing override
     if (force != nullptr && *force != '\0') {
         const int f = std::atoi(force);
-        if (f >= 0 && f < kNumConfigs && !(f == 2 && e == 1)) cfg = f;
+        if (f >= 0 && f < kNumConfigs) cfg = f;
     }
     if (n128_only) cfg = 2;
     const bool forced = cfg >= 0;
@@ -663,17 +663,18 @@ int gemm_tiled_plan(int dtype, int64_t M, int64_t N, int64_t K, const DeviceProp
     //   partials (s > 1): the fp32 partials written and read back,
     //            2 * s * M * N * 4 bytes at ~5 TB/s, plus ~5 us for the
     //            reduction's launch.
-    // time(s) = max(MFMA, stream) + partials; the smallest time wins. For
-    // 16-bit inputs the model rates both 128-row configurations, 128 x 256
-    // and 128 x 128 tiles (twice the blocks for the same B traffic: skinny
-    // and few-tile shapes fill the CUs with fewer K splits), keeping 128 x 256
-    // on a tie. Against the previous choice of 128 x 256 tiles alone it ran
-    // every shape it changes faster on MI355X, bf16: 16..256 x 8192 x 8192
-    // by 2-7%, 128 x 4096 x 4096 by 21%, 256 x 512 x 1024 by 34%.
+    // time(s) = max(MFMA, stream) + partials; the smallest time wins. The
+    // model rates both 128-row configurations, 128 x 256 and 128 x 128 tiles
+    // (twice the blocks for the same B traffic: skinny and few-tile shapes
+    // fill the CUs with fewer K splits), keeping 128 x 256 on a tie. Against
+    // the previous choice of 128 x 256 tiles alone it ran every bf16 shape it
+    // changes faster on MI355X (16..256 x 8192 x 8192 by 2-7%, 128 x 4096 x
+    // 4096 by 21%, 256 x 512 x 1024 by 34%) and 12 of 13 fp8 shapes (up to
+    // 30%; 16 x 8192 x 8192 fp8 5% slower).
     int splits = 1;
     if (kConfigs[cfg].bm == 128) {
         const int cands[2] = {cfg, 2};
-        const int n_cands = (!forced && cfg == 1 && e == 2) ? 2 : 1;
+        const int n_cands = (!forced && cfg == 1) ? 2 : 1;
         const double flops_per_cu = 6.0e12 * (e == 1 ? 2.0 : 1.0), bw = 5.0e12;
         double best = -1.0;
         int best_cfg = cfg;

@@ -72,16 +72,12 @@ def test_gemm_random_matches_fp32_matmul(lib, dtype, shape):
 @pytest.mark.parametrize("shape", [(256, 256, 128), (256, 512, 64), (256, 512, 1024), (512, 256, 4096), (768, 1280, 384)])
 def test_tiled_configurations(lib, dtype, config, shape, monkeypatch):
     # Every tiled configuration on shapes it divides, selected through the
-    # configuration override; the plan names the kernel that ran. The
-    # 128 x 128 configuration takes 16-bit inputs only (fp8 keeps its default).
+    # configuration override; the plan names the kernel that ran.
     monkeypatch.setenv("MB_GEMM_TILED_CONFIG", config)
     m, n, k = shape
     info = lib.gemm_info(capi.DTYPES[dtype], m, n, k)
     assert info["implementation"] == "gfx950_mfma32_lds_dma"
-    if config == "2" and dtype.startswith("float8"):
-        assert info["tile_n"] == 256
-    else:
-        assert (info["tile_m"], info["tile_n"]) == {"0": (256, 256), "1": (128, 256), "2": (128, 128)}[config]
+    assert (info["tile_m"], info["tile_n"]) == {"0": (256, 256), "1": (128, 256), "2": (128, 128)}[config]
     print(f"[gemm] tiled cfg {config} {dtype} {shape}", flush=True)
     _check_random(lib, dtype, m, n, k, seed=k)
 
@@ -93,8 +89,6 @@ def test_tiled_stage_counts(lib, dtype, config, ksteps, monkeypatch):
     # A is loaded two 64-byte K stages at a time: odd stage counts leave the
     # last pair half used, and counts around the 12-step unroll exercise the
     # tail loads that re-read the last stage / pair.
-    if config == "2" and dtype.startswith("float8"):
-        pytest.skip("128 x 128 tiles take 16-bit inputs only")
     monkeypatch.setenv("MB_GEMM_TILED_CONFIG", config)
     monkeypatch.setenv("MB_GEMM_SPLITS", "1")  # the 128-row tiles would split K for this few tiles
     k = ksteps * (64 if dtype.startswith("float8") else 32)
@@ -118,10 +112,10 @@ def test_forced_splits_with_odd_stage_counts(lib, dtype, splits, ksteps, monkeyp
     _check_random(lib, dtype, m, n, k, seed=splits)
 
 
-@pytest.mark.parametrize("dtype", ["bfloat16", "float16"])
+@pytest.mark.parametrize("dtype", LOWP)
 @pytest.mark.parametrize("shape", [(512, 384, 256), (1000, 1152, 320), (64, 640, 512), (16, 1152, 4096), (3, 128, 64)])
 def test_n_multiple_of_128_takes_128x128_tiles(lib, dtype, shape, monkeypatch):
-    # 16-bit shapes with N a multiple of 128 but not 256 run the pipelined kernel on 128 x 128 tiles
+    # Shapes with N a multiple of 128 but not 256 run the pipelined kernel on 128 x 128 tiles
     # (ragged M through the buffer range checks, skinny shapes with K splits).
     monkeypatch.setenv("MB_GEMM_NO_GEMV", "1")  # keep M <= 4 on the tiled kernel too
     m, n, k = shape
@@ -129,13 +123,6 @@ def test_n_multiple_of_128_takes_128x128_tiles(lib, dtype, shape, monkeypatch):
     assert info["implementation"] == "gfx950_mfma32_lds_dma" and (info["tile_m"], info["tile_n"]) == (128, 128)
     print(f"[gemm] n%128 {dtype} {shape} split {info['split_k']}", flush=True)
     _check_random(lib, dtype, m, n, k, seed=n + 3)
-
-
-@pytest.mark.parametrize("dtype", ["float8_e4m3fn", "float8_e5m2"])
-def test_fp8_n_multiple_of_128_only_uses_the_generic_kernel(lib, dtype):
-    info = lib.gemm_info(capi.DTYPES[dtype], 512, 384, 256)
-    assert info["implementation"] != "gfx950_mfma32_lds_dma"
-    _check_random(lib, dtype, 512, 384, 256, seed=2)
 
 
 @pytest.mark.parametrize("dtype", ["bfloat16", "float16"])
@@ -164,10 +151,11 @@ def test_skinny_benchmark_shapes_split_two_ways_on_128x128_tiles(lib, dtype, sha
 
 
 @pytest.mark.parametrize("dtype", ["float8_e4m3fn", "float8_e5m2"])
-def test_fp8_skinny_keeps_128x256_tiles(lib, dtype):
-    # fp8 has no 128 x 128 configuration: the model rates 128 x 256 tiles only.
+def test_fp8_skinny_takes_128x128_tiles(lib, dtype):
+    # As for 16-bit inputs, the model picks 2 splits over 128 x 128 tiles for the skinny shape.
     info = lib.gemm_info(capi.DTYPES[dtype], 128, 8192, 8192)
-    assert (info["tile_m"], info["tile_n"], info["split_k"]) == (128, 256, 4)
+    assert (info["tile_m"], info["tile_n"], info["split_k"]) == (128, 128, 2)
+    _check_random(lib, dtype, 128, 8192, 8192, seed=5, rows=64)
 
 
 @pytest.mark.parametrize("dtype", LOWP)

@@ -84,13 +84,14 @@ def b_tr16_addrs(row_bytes: int, nb: int, s: int, t: int) -> list[int]:
     return out
 
 
-def b_tr8_addrs(nb: int, t: int) -> list[int]:
+def b_tr8_addrs(nb: int, t: int, row_bytes: int = 256) -> list[int]:
     out = []
     for lane in range(64):
         g, i = lane >> 4, lane & 15
         k = 32 * (g >> 1) + 8 * t + (i >> 1)
         n = nb + 16 * (g & 1) + 8 * (i & 1)
-        out.append(k * 256 + (((n >> 4) ^ swz_b8(k & 7)) << 4) + 8 * (i & 1))
+        f = swz_b8(k & 7) if row_bytes == 256 else k & 7  # 128-byte rows (128 columns): f = k
+        out.append(k * row_bytes + (((n >> 4) ^ f) << 4) + 8 * (i & 1))
     return out
 
 
@@ -102,11 +103,12 @@ def test_b_transposing_reads_are_conflict_free():
                     addrs = b_tr16_addrs(row_bytes, nb, s, t)
                     assert worst_lanes_per_bank(addrs, 8, 16, 32) == 1
                     assert worst_lanes_per_bank(addrs, 8, 32, 64) == 1
-    for nb in range(0, 256, 32):
-        for t in range(4):
-            addrs = b_tr8_addrs(nb, t)
-            assert worst_lanes_per_bank(addrs, 8, 16, 32) == 1
-            assert worst_lanes_per_bank(addrs, 8, 32, 64) == 1
+    for row_bytes in (256, 128):
+        for nb in range(0, row_bytes, 32):
+            for t in range(4):
+                addrs = b_tr8_addrs(nb, t, row_bytes)
+                assert worst_lanes_per_bank(addrs, 8, 16, 32) == 1
+                assert worst_lanes_per_bank(addrs, 8, 32, 64) == 1
 
 
 @pytest.mark.parametrize("bm, waves", [(256, 4), (128, 4)])
