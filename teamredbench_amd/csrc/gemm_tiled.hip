@@ -463,11 +463,13 @@ gemm_tiled_kernel(const unsigned char* __restrict__ A, const unsigned char* __re
     // from registers, every store instruction would put 16 bytes into each of
     // 32 rows. Instead each wave rounds its (WTM x WTN) tile to 16 bits into
     // its own region of the LDS ring (all of it is free after the final wait
-    // and barrier), then reads it back row by row so that 16 lanes store one
-    // 256-byte row segment: whole cache lines, half the store instructions.
-    // Staged rows are 16 chunks of 16 bytes; chunk c of row r sits at chunk
-    // c ^ (r % 16), which keeps both the writes (32 rows, one chunk) and the
-    // reads (4 rows, all chunks) free of bank conflicts. Rows at or past M (a
+    // and barrier), then reads it back row by row so that 16 (8) lanes store
+    // one 256-byte (128-byte) row segment of a 128- (64-) column wave tile:
+    // whole cache lines, half the store instructions. Staged rows are 16 (8)
+    // chunks of 16 bytes; chunk c of row r sits at chunk c ^ (r % chunks),
+    // which keeps the reads (all chunks of a few rows) free of bank conflicts;
+    // the writes (one chunk of 32 rows) conflict 2-way, since each half wave
+    // fills only one 8-byte half of every chunk. Rows at or past M (a
     // partial last tile) are not stored. With K splits the block writes its
     // unscaled fp32 partial to ws[split][row][col] directly; a second kernel
     // sums the splits.
@@ -476,7 +478,7 @@ gemm_tiled_kernel(const unsigned char* __restrict__ A, const unsigned char* __re
     if (ws == nullptr) {
         constexpr int ROW_BYTES = WTN * 2;
         constexpr int ROW_CHUNKS = ROW_BYTES / 16;
-        static_assert(ROW_CHUNKS == 16, "staging swizzle assumes 256-byte rows");
+        static_assert(ROW_CHUNKS == 16 || ROW_CHUNKS == 8, "staging covers wave tiles 128 or 64 columns wide");
         static_assert(W * WTM * ROW_BYTES <= LDS_BYTES, "the waves' tiles must fit the LDS ring");
         unsigned char* stage = lds + wave * WTM * ROW_BYTES;
         // alpha is 1 except for scaled fp8: the unscaled instantiation skips
@@ -578,7 +580,7 @@ struct TiledConfig {
 constexpr TiledConfig kConfigs[] = {
     {256, 256, 2, 2, 3, 4, 4},  // 0: large problems, 128 x 128 per wave; 3 x 32 + 4 x 16 KiB
     {128, 256, 2, 2, 3, 6, 8},  // 1: mid-size problems, 64 x 128 per wave; 3 x 16 + 6 x 16 KiB
-    {128, 128, 4, 1, 3, 6, 4},  // 2: few tiles, N % 256 != 0: 32 x 128 per wave; 3 x 16 + 6 x 8 KiB
+    {128, 128, 2, 2, 3, 6, 4},  // 2: few tiles, N % 256 != 0: 64 x 64 per wave; 3 x 16 + 6 x 8 KiB
 };
 constexpr int kNumConfigs = sizeof(kConfigs) / sizeof(kConfigs[0]);
 
