@@ -165,6 +165,54 @@ constexpr LoadSchedule load_schedule(int NA, int NB, int AI, int BI) {
     return r;
 }
 
+// Issue order and vmcnt waits of the fp8 16x16x128 kernel's ring. B stage S
+// is read into registers during step S - 2 (stages 0 and 1 before step 0)
+// and A pair P during steps 2P - 1 .. 2P + 1. Step k issues, in this order,
+// A pair k / 2 + NA - 1 when k is even (AI loads per wave) and B stage
+// k + 1 + NB (BI loads); the prologue issues pairs 0..NA-2 and stages
+// 0..NB-1 by the same rule over the steps before step 0, then, once stages
+// 0 and 1 are read and a barrier has freed stage 0's slot, stage NB. Before
+// step j the pipeline needs B stage j + 2 and A pair (j + 1) / 2.
+constexpr int floor_half(int v) { return v >= 0 ? v / 2 : -((1 - v) / 2); }
+
+constexpr LoadSchedule load_schedule_mi16(int NA, int NB, int AI, int BI, bool split_a) {
+    constexpr int kSteps = 64;
+    int end_a[kSteps + 16] = {}, end_b[kSteps + 16] = {}, issued_before[kSteps] = {};
+    int total = 0;
+    // A loads of step (or virtual step) v: all AI of pair v / 2 + NA - 1 on
+    // even v, or, split, AI / 2 of pair floor(v / 2) + NA - 1 on every v.
+    auto a_step = [&](int v) {
+        const int pair = floor_half(v) + NA - 1;
+        if (pair < 0 || pair >= kSteps + 16) return;
+        if (split_a) total += AI / 2;
+        else if ((v & 1) == 0) total += AI;
+        else return;
+        end_a[pair] = total;
+    };
+    const int V = NB + 1 > 2 * NA - 2 ? NB + 1 : 2 * NA - 2;
+    for (int v = -V; v < 0; ++v) {
+        a_step(v);
+        if (v + 1 + NB >= 0 && v + 1 + NB < NB) end_b[v + 1 + NB] = (total += BI);
+    }
+    LoadSchedule r{1 << 20, 1 << 20, 0};
+    int p0 = end_a[0] > end_b[0] ? end_a[0] : end_b[0];
+    p0 = p0 > end_b[1] ? p0 : end_b[1];
+    r.prologue = total - p0;
+    end_b[NB] = (total += BI);
+    for (int k = 0; k < kSteps; ++k) {
+        issued_before[k] = total;
+        a_step(k);
+        if (k + 1 + NB < kSteps + 16) end_b[k + 1 + NB] = (total += BI);
+    }
+    for (int j = 0; j + 2 < kSteps; ++j) {
+        const int need = end_a[(j + 1) / 2] > end_b[j + 2] ? end_a[(j + 1) / 2] : end_b[j + 2];
+        const int w = issued_before[j] - need;
+        if (j & 1) r.odd_wait = w < r.odd_wait ? w : r.odd_wait;
+        else r.even_wait = w < r.even_wait ? w : r.even_wait;
+    }
+    return r;
+}
+
 // One transposing read of this lane's B operand (column nb + lane % 32).
 // 16-bit: 4 K-rows x 16 columns per 16-lane group, part t (0..1) of substep s
 // gives K 16s + 8*(lane/32) + 4t .. +3. fp8: 8 K-rows x 16 columns, part t
@@ -200,6 +248,42 @@ __device__ __forceinline__ u32x2 pack4(float a, float b, float c, float d) {
     } else {
         bf16x4 h = {(__bf16)a, (__bf16)b, (__bf16)c, (__bf16)d};
         return __builtin_bit_cast(u32x2, h);
+    }
+}
+
+// Second half of the epilogue: a wave's (WTM x ROW_BYTES / 2) tile, staged in
+// LDS as 16-bit values (chunk c of row r at chunk c ^ (r % chunks)), read back
+// row by row and stored so that 16 (8) lanes write one 256-byte (128-byte) C
+// row segment: whole cache lines. Read-backs go out in batches of BATCH
+// before their stores, so no store waits on the LDS read just before it.
+// Rows at or past M (a partial last tile) are not stored.
+template <int WTM, int ROW_BYTES>
+__device__ __forceinline__ void store_staged_tile(const unsigned char* stage, unsigned char* C, int M, int N,
+                                                  int row_base, int64_t col_base, int lane) {
+    constexpr int ROW_CHUNKS = ROW_BYTES / 16;
+    const int64_t ldc = (int64_t)N * 2;  // bytes per C row (16-bit output)
+    constexpr int ROWS_PER_STORE = 64 / ROW_CHUNKS;
+    constexpr int STORES = WTM / ROWS_PER_STORE;
+    constexpr int BATCH = 8;
+    static_assert(STORES % BATCH == 0, "stores split into batches");
+    const int c = lane % ROW_CHUNKS;
+    const int r0 = lane / ROW_CHUNKS;
+    int grow = row_base + r0;
+    unsigned char* cptr = C + (int64_t)grow * ldc + col_base * 2 + c * 16;
+#pragma unroll
+    for (int p0 = 0; p0 < STORES; p0 += BATCH) {
+        u32x4 rows[BATCH];
+#pragma unroll
+        for (int p = 0; p < BATCH; ++p) {
+            const int r = ROWS_PER_STORE * (p0 + p) + r0;
+            rows[p] = *reinterpret_cast<const u32x4*>(stage + r * ROW_BYTES + ((c ^ (r % ROW_CHUNKS)) << 4));
+        }
+#pragma unroll
+        for (int p = 0; p < BATCH; ++p) {
+            if (grow < M) *reinterpret_cast<u32x4*>(cptr) = rows[p];
+            grow += ROWS_PER_STORE;
+            cptr += ROWS_PER_STORE * ldc;
+        }
     }
 }
 
@@ -506,32 +590,7 @@ gemm_tiled_kernel(const unsigned char* __restrict__ A, const unsigned char* __re
             }
         };
         stage_tile(std::integral_constant<bool, SCALED>{});
-        // Read-backs go out in batches of BATCH before their stores, so no
-        // store waits on the LDS read just before it.
-        const int64_t ldc = (int64_t)N * 2;  // bytes per C row (16-bit output)
-        constexpr int ROWS_PER_STORE = 64 / ROW_CHUNKS;
-        constexpr int STORES = WTM / ROWS_PER_STORE;
-        constexpr int BATCH = 8;
-        static_assert(STORES % BATCH == 0, "stores split into batches");
-        const int c = lane % ROW_CHUNKS;
-        const int r0 = lane / ROW_CHUNKS;
-        int grow = tm * BM + wm * WTM + r0;
-        unsigned char* cptr = C + (int64_t)grow * ldc + ((int64_t)tn * BN + wn * WTN) * 2 + c * 16;
-#pragma unroll
-        for (int p0 = 0; p0 < STORES; p0 += BATCH) {
-            u32x4 rows[BATCH];
-#pragma unroll
-            for (int p = 0; p < BATCH; ++p) {
-                const int r = ROWS_PER_STORE * (p0 + p) + r0;
-                rows[p] = *reinterpret_cast<const u32x4*>(stage + r * ROW_BYTES + ((c ^ (r % ROW_CHUNKS)) << 4));
-            }
-#pragma unroll
-            for (int p = 0; p < BATCH; ++p) {
-                if (grow < M) *reinterpret_cast<u32x4*>(cptr) = rows[p];
-                grow += ROWS_PER_STORE;
-                cptr += ROWS_PER_STORE * ldc;
-            }
-        }
+        store_staged_tile<WTM, ROW_BYTES>(stage, C, M, N, tm * BM + wm * WTM, (int64_t)tn * BN + wn * WTN, lane);
     } else {
         float* part = ws + (int64_t)split * M * N;
 #pragma unroll
@@ -547,6 +606,328 @@ gemm_tiled_kernel(const unsigned char* __restrict__ A, const unsigned char* __re
                     *reinterpret_cast<f32x4*>(prow + col0 + 32 * j + 8 * g) = q;
                 }
             }
+        }
+    }
+}
+
+// fp8 (e4m3 / e5m2) on v_mfma_scale_f32_16x16x128_f8f6f4, which sustains 7-8%
+// more than the 32x32x64 form under the part's power limit. Same LDS ring,
+// DMA loads, A pair layout and XCD tile order as gemm_tiled_kernel; what
+// differs:
+//  - Operand K layout. The instruction pairs byte b of lane l of one operand
+//    with byte b of lane l of the other (both hold K in the same places), so
+//    any K order shared by A and B gives the same dot product. Here lane l,
+//    g = l / 16, holds K 16g .. 16g + 15 in bytes 0-15 and K 64 + 16g ..
+//    64 + 16g + 15 in bytes 16-31: bytes 0-15 come from the first stage of a
+//    pair and bytes 16-31 from the second, so B is still read one stage at a
+//    time. A: two 16-byte reads (chunks g and 4 + g of the pair row). B: per
+//    stage two transposing reads (8 K rows x 16 columns per 16-lane group).
+//  - Steps. One MFMA consumes a whole pair (128 K), so the two steps of pair p
+//    share its MFMAs: step 2p does fragment rows 0 .. FM/2 - 1, step 2p + 1
+//    the rest. B fragments of pair p + 1 are read during pair p's steps (stage
+//    k + 2 during step k, into the other of two B register sets); A fragment
+//    rows stream one row ahead (row i + 1 is read after the first MFMA of row
+//    i, row 0 of the next pair during the last row).
+//  - Ring. B stage S lives in slot S % NB and is read during step S - 2; A
+//    pair P in slot P % NA, read during steps 2P - 1 .. 2P + 1. Step k loads
+//    A pair k / 2 + NA - 1 (even k) into the slot pair k / 2 - 1 vacated, and
+//    B stage k + 1 + NB into the slot of stage k + 1; waits from
+//    load_schedule_mi16.
+//  - fp8 B rows: chunk c of row k stored at c ^ f(k), f = swz_b8(k & 7) ^ bit 4
+//    of k (256-byte rows) or (k & 7) ^ bit 4 of k (128-byte rows): the two
+//    16-lane groups of a 32-lane LDS phase read rows 16 apart.
+// Requires an even number of stages per split.
+constexpr int kMi16AAhead = 1;              // A fragment rows read this far ahead
+constexpr bool kMi16SpreadLoads = true;     // DMA loads spread over the step, or first
+constexpr bool kMi16SplitA = false;         // an A pair's loads over both steps of a pair, or the even one
+
+__device__ __forceinline__ int swz_b8_mi16(int k, int row_bytes) {
+    return (row_bytes == 256 ? swz_b8(k & 7) : (k & 7)) ^ ((k >> 4) & 1);
+}
+
+template <int DT>
+__device__ __forceinline__ f32x4 mfma16_fp8(const i32x8& a, const i32x8& b, f32x4 c) {
+    constexpr int fmt = DT == MB_DT_FLOAT8_E5M2 ? 1 : 0;  // 0 = e4m3, 1 = bf8 e5m2
+    return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, fmt, fmt, 0, 0, 0, 0);
+}
+
+template <int DT, int BM, int BN, int WGM, int WGN, int NA, int NB, bool SCALED>
+__global__ void __launch_bounds__(64 * WGM * WGN)
+gemm_fp8_mi16_kernel(const unsigned char* __restrict__ A, const unsigned char* __restrict__ B,
+                     unsigned char* __restrict__ C, int M, int N, int K, float alpha, int tiles_m, int tiles_n,
+                     int group_m, int splits, int k_len, float* __restrict__ ws) {
+    constexpr int W = WGM * WGN;
+    constexpr int WTM = BM / WGM, WTN = BN / WGN;
+    constexpr int FM = WTM / 16, FN = WTN / 16;
+    constexpr int HALF_ROWS = FM / 2;                   // fragment rows per step
+    constexpr int PAIR = 2 * BM * kStageK;              // A slot: two stages, [BM][128 B]
+    constexpr int B_ROW = BN;                           // bytes per B row (fp8)
+    constexpr int B_BYTES = kStageK * B_ROW;            // B slot: one stage, 64 K rows
+    constexpr int A_INSTR = PAIR / 1024 / W;
+    constexpr int B_INSTR = B_BYTES / 1024 / W;
+    constexpr int RPI = 1024 / B_ROW;                   // B rows per DMA instruction
+    constexpr int LDS_BYTES = NA * PAIR + NB * B_BYTES;
+    static_assert(W == 4 && FM % 2 == 0 && FN >= 2, "four waves, an even number of fragment rows");
+    static_assert(B_ROW == 256 || B_ROW == 128, "fp8 B rows of 256 or 128 bytes");
+    static_assert(A_INSTR % 2 == 0 && B_INSTR % 2 == 0 && B_INSTR * RPI * W == kStageK,
+                  "A and B offsets assume two vector offsets per wave");
+    static_assert(NA >= 2 && NB >= 3 && LDS_BYTES <= 160 * 1024, "LDS ring does not fit");
+    constexpr LoadSchedule kSched = load_schedule_mi16(NA, NB, A_INSTR, B_INSTR, kMi16SplitA);
+    static_assert(kSched.prologue >= 0 && kSched.odd_wait >= 0 && kSched.even_wait >= 0 &&
+                  kSched.prologue < 64 && kSched.odd_wait < 64 && kSched.even_wait < 64,
+                  "load schedule leaves a needed stage unissued or overflows vmcnt");
+
+    __shared__ __attribute__((aligned(1024))) unsigned char lds[LDS_BYTES];
+    auto a_slot = [&](auto idx) -> unsigned char* {
+        static_assert(decltype(idx)::value < NA, "A slot out of range");
+        return lds + decltype(idx)::value * PAIR;
+    };
+    auto b_slot = [&](auto idx) -> unsigned char* {
+        static_assert(decltype(idx)::value < NB, "B slot out of range");
+        return lds + NA * PAIR + decltype(idx)::value * B_BYTES;
+    };
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int g = lane >> 4, l16 = lane & 15;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave / WGN, wn = wave % WGN;
+    const int split = splits > 1 ? (int)blockIdx.x % splits : 0;
+    const int tile = splits > 1 ? (int)blockIdx.x / splits : (int)blockIdx.x;
+    int tm, tn;
+    tile_coords(tile, tiles_m * tiles_n, tiles_m, tiles_n, group_m, &tm, &tn);
+    const int lda = K, ldb = N;
+    const int k0 = split * k_len;
+
+    const int a_rows = min(BM, M - tm * BM);
+    const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<unsigned char*>(A) + (int64_t)tm * BM * lda, (short)0, a_rows * lda, kBufferFlags);
+    const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<unsigned char*>(B) + (int64_t)tn * BN, (short)0, K * ldb, kBufferFlags);
+
+    // DMA offsets: instruction q of a wave covers A rows 8 * (wave * A_INSTR
+    // + q) .. +7 (whole 128-byte pair rows) and B rows RPI * (wave * B_INSTR +
+    // q) .. +RPI-1 of the stage. Both swizzles depend on q only through its
+    // parity (the B rows of a wave share bit 4), so two vector offsets per
+    // operand serve every q; the rest is a uniform offset.
+    int a_voff[2], b_voff[2];
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+        const int lin = (wave * A_INSTR + q) * 1024 + lane * 16;
+        const int row = lin / (2 * kStageK), pchunk = (lin % (2 * kStageK)) >> 4;
+        a_voff[q] = row * lda + ((pchunk ^ swz_a2(row)) << 4);
+        const int blin = (wave * B_INSTR + q) * 1024 + lane * 16;
+        const int brow = blin / B_ROW, bchunk = (blin % B_ROW) >> 4;
+        b_voff[q] = brow * ldb + ((bchunk ^ swz_b8_mi16(brow, B_ROW)) << 4);
+    }
+    auto issue_a = [&](int pair, unsigned char* slot, auto idx) {
+        constexpr int q = decltype(idx)::value;
+        const unsigned base = (unsigned)(uintptr_t)(MB_LDS unsigned char*)slot;
+        lds_dma16(ra, base + (wave * A_INSTR + q) * 1024, a_voff[q & 1], k0 + pair * 2 * kStageK + 16 * (q >> 1) * lda);
+    };
+    auto issue_b = [&](int kt, unsigned char* slot, auto idx) {
+        constexpr int q = decltype(idx)::value;
+        const unsigned base = (unsigned)(uintptr_t)(MB_LDS unsigned char*)slot;
+        lds_dma16(rb, base + (wave * B_INSTR + q) * 1024, b_voff[q & 1],
+                  (k0 + kt * kStageK + 2 * RPI * (q >> 1)) * ldb);
+    };
+
+    // Operand reads. A fragment row i (16 rows): chunks g and 4 + g of the
+    // pair row. B fragment j, stage half h, part t: 8 K rows 16g + 8t .. +7
+    // of the stage, columns b_col + 16j .. +15, into bytes 16h + 8t .. +7.
+    // Per-lane byte offsets within a slot: the A swizzle of row a_row + 16i
+    // equals that of l16 (wm * WTM and 16i leave bits 0-3 alone), and the B
+    // swizzle of row 16g + 8t + l16 / 2 does not depend on t, so two A offsets
+    // and one B offset per fragment column serve every read; rows and parts
+    // are immediates.
+    const int a_row = wm * WTM + l16;
+    const int b_col = wn * WTN;
+    const int sa = swz_a2(l16);
+    int a_off[2] = {a_row * 2 * kStageK + ((g ^ sa) << 4), a_row * 2 * kStageK + (((4 + g) ^ sa) << 4)};
+    const int kb = 16 * g + (l16 >> 1);
+    int b_off[FN];
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+        b_off[j] = kb * B_ROW + ((((b_col >> 4) + j) ^ swz_b8_mi16(kb, B_ROW)) << 4) + 8 * (l16 & 1);
+    // Slot bases past 64 KiB do not fit the LDS instructions' offset field;
+    // redefining the offsets once per step (an empty asm) keeps the compiler
+    // from hoisting a register per (slot, offset) out of the loop.
+    auto launder_offsets = [&] {
+        asm volatile("" : "+v"(a_off[0]), "+v"(a_off[1]));
+#pragma unroll
+        for (int j = 0; j < FN; ++j) asm volatile("" : "+v"(b_off[j]));
+    };
+    auto read_a = [&](const unsigned char* slot, int i, i32x8& dst) {
+        const u32x4 lo = *reinterpret_cast<const u32x4*>(slot + a_off[0] + i * 16 * 2 * kStageK);
+        const u32x4 hi = *reinterpret_cast<const u32x4*>(slot + a_off[1] + i * 16 * 2 * kStageK);
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            dst[w] = (int)lo[w];
+            dst[4 + w] = (int)hi[w];
+        }
+    };
+    auto read_b = [&](const unsigned char* st, int j, int h, int t, i32x8& dst) {
+        const i32x2_t v = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
+            (MB_LDS i32x2_t*)((MB_LDS unsigned char*)st + b_off[j] + t * 8 * B_ROW));
+        dst[4 * h + 2 * t] = v[0];
+        dst[4 * h + 2 * t + 1] = v[1];
+    };
+
+    f32x4 acc[FM][FN];
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    // A fragment rows are read A_AHEAD rows before their MFMAs, into a ring
+    // of A_AHEAD + 1 registers sets indexed by the row's position in the
+    // unrolled loop (pair * FM + row).
+    constexpr int A_AHEAD = kMi16AAhead;
+    i32x8 bop[2][FN];              // B fragments of the current and the next pair
+    i32x8 aop[A_AHEAD + 1];
+
+    const int ksteps = k_len / kStageK;  // even
+    const int last = ksteps - 1;
+    const int last_pair = last / 2;
+    // Prologue: virtual steps -V..-1 issue A pairs 0..NA-2 and B stages 0..NB-1.
+    constexpr int V = NB + 1 > 2 * NA - 2 ? NB + 1 : 2 * NA - 2;
+    [&]<int... U>(std::integer_sequence<int, U...>) {
+        ([&] {
+            constexpr int v = U - V;
+            constexpr int pair = floor_half(v) + NA - 1;
+            if constexpr (pair >= 0 && (kMi16SplitA || (v & 1) == 0)) {
+                constexpr int q0 = kMi16SplitA && (v & 1) != 0 ? A_INSTR / 2 : 0;
+                constexpr int nq = kMi16SplitA ? A_INSTR / 2 : A_INSTR;
+                [&]<int... Q>(std::integer_sequence<int, Q...>) {
+                    (issue_a(min(pair, last_pair), a_slot(std::integral_constant<int, pair>{}),
+                             std::integral_constant<int, q0 + Q>{}), ...);
+                }(std::make_integer_sequence<int, nq>{});
+            }
+            if constexpr (v + 1 + NB >= 0 && v + 1 + NB < NB) {
+                constexpr int st = v + 1 + NB;
+                [&]<int... Q>(std::integer_sequence<int, Q...>) {
+                    (issue_b(min(st, last), b_slot(std::integral_constant<int, st>{}),
+                             std::integral_constant<int, Q>{}), ...);
+                }(std::make_integer_sequence<int, B_INSTR>{});
+            }
+        }(), ...);
+    }(std::make_integer_sequence<int, V>{});
+    wait_vmcnt_and_barrier<kSched.prologue>();
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            read_b(b_slot(std::integral_constant<int, 0>{}), j, 0, t, bop[0][j]);
+            read_b(b_slot(std::integral_constant<int, 1>{}), j, 1, t, bop[0][j]);
+        }
+#pragma unroll
+    for (int i = 0; i < A_AHEAD; ++i) read_a(a_slot(std::integral_constant<int, 0>{}), i, aop[i]);
+    // Every wave has read stage 0: its slot takes stage NB.
+    wait_vmcnt_and_barrier<63>();
+    [&]<int... Q>(std::integer_sequence<int, Q...>) {
+        (issue_b(min(NB, last), b_slot(std::integral_constant<int, 0>{}), std::integral_constant<int, Q>{}), ...);
+    }(std::make_integer_sequence<int, B_INSTR>{});
+
+    auto step = [&](auto idx, int kt) {
+        constexpr int I = decltype(idx)::value;
+        constexpr int H = I & 1;                  // which half of the pair's fragment rows
+        constexpr int CUR = (I / 2) & 1;          // B register set of this pair
+        constexpr int A_LOADS = kMi16SplitA ? A_INSTR / 2 : H == 0 ? A_INSTR : 0;
+        constexpr int A_Q0 = kMi16SplitA && H == 1 ? A_INSTR / 2 : 0;   // first A instruction of this step
+        constexpr int LOADS = A_LOADS + B_INSTR;
+        constexpr int N_MFMA = HALF_ROWS * FN;
+        constexpr int N_OTHER = LOADS + 2 * FN;   // loads first, then this stage's next-pair B reads
+        constexpr int PER = (N_OTHER + N_MFMA - 1) / N_MFMA;
+        const unsigned char* a_cur = a_slot(std::integral_constant<int, (I / 2) % NA>{});
+        const unsigned char* a_next = a_slot(std::integral_constant<int, (I / 2 + 1) % NA>{});
+        const unsigned char* b_read = b_slot(std::integral_constant<int, (I + 2) % NB>{});
+        unsigned char* a_load = a_slot(std::integral_constant<int, (I / 2 + NA - 1) % NA>{});
+        unsigned char* b_load = b_slot(std::integral_constant<int, (I + 1) % NB>{});
+        wait_vmcnt_and_barrier<H ? kSched.odd_wait : kSched.even_wait>();
+        launder_offsets();
+        const int aload = min((kt >> 1) + NA - 1, last_pair);
+        const int bload = min(kt + 1 + NB, last);
+        // Other memory instruction m is a load when m + 1 is one of the first
+        // LOADS multiples of kStride (spread evenly), otherwise the next B read.
+        constexpr int kStride = kMi16SpreadLoads ? N_OTHER / LOADS : 1;
+        constexpr auto kIsLoad = [](int m) { return (m + 1) % kStride == 0 && (m + 1) / kStride <= LOADS; };
+        [&]<int... Q>(std::integer_sequence<int, Q...>) {
+            ([&] {
+                constexpr int i = H * HALF_ROWS + Q / FN, j = Q % FN;
+                constexpr int row_pos = (I / 2) * FM + i;   // position in the unrolled loop
+                acc[i][j] = mfma16_fp8<DT>(bop[CUR][j], aop[row_pos % (A_AHEAD + 1)], acc[i][j]);
+                if constexpr (j == 0) {
+                    constexpr int ahead = (row_pos + A_AHEAD) % (A_AHEAD + 1);
+                    if constexpr (i + A_AHEAD < FM) read_a(a_cur, i + A_AHEAD, aop[ahead]);
+                    else read_a(a_next, i + A_AHEAD - FM, aop[ahead]);
+                }
+                constexpr int lo = Q * PER < N_OTHER ? Q * PER : N_OTHER;
+                constexpr int hi = Q * PER + PER < N_OTHER ? Q * PER + PER : N_OTHER;
+                [&]<int... R>(std::integer_sequence<int, R...>) {
+                    ([&] {
+                        constexpr int m = lo + R;
+                        if constexpr (kIsLoad(m)) {
+                            constexpr int l = (m + 1) / kStride - 1;
+                            if constexpr (l < A_LOADS) issue_a(aload, a_load, std::integral_constant<int, A_Q0 + l>{});
+                            else issue_b(bload, b_load, std::integral_constant<int, l - A_LOADS>{});
+                        } else {
+                            constexpr int loads_before = m / kStride < LOADS ? m / kStride : LOADS;
+                            constexpr int r = m - loads_before;
+                            read_b(b_read, r / 2, H, r % 2, bop[CUR ^ 1][r / 2]);
+                        }
+                    }(), ...);
+                }(std::make_integer_sequence<int, hi - lo>{});
+                __builtin_amdgcn_sched_barrier(0);
+            }(), ...);
+        }(std::make_integer_sequence<int, N_MFMA>{});
+    };
+    // The stage count is even: both steps of a pair run or neither, so every
+    // register set is whole wherever control flow joins.
+    constexpr int UNROLL = std::lcm(std::lcm(2 * NA, NB), 4);
+    static_assert((UNROLL / 2) * FM % (A_AHEAD + 1) == 0, "A register ring must wrap with the unrolled loop");
+    for (int kt = 0; kt < ksteps; kt += UNROLL) {
+        [&]<int... P>(std::integer_sequence<int, P...>) {
+            ((kt + 2 * P < ksteps ? (step(std::integral_constant<int, 2 * P>{}, kt + 2 * P),
+                                     step(std::integral_constant<int, 2 * P + 1>{}, kt + 2 * P + 1))
+                                  : void()), ...);
+        }(std::make_integer_sequence<int, UNROLL / 2>{});
+    }
+    wait_vmcnt_and_barrier<0>();
+
+    // Epilogue. Accumulator register r of fragment (i, j) of lane l holds
+    // C[16i + l % 16][16j + 4(l / 16) + r]: four consecutive columns of one
+    // row, rounded to 16 bits into the wave's LDS staging rows and stored as
+    // whole row segments (store_staged_tile). With K splits the block writes
+    // its unscaled fp32 partial to ws[split][row][col] instead.
+    if (ws == nullptr) {
+        constexpr int ROW_BYTES = WTN * 2;
+        constexpr int ROW_CHUNKS = ROW_BYTES / 16;
+        static_assert(ROW_CHUNKS == 16 || ROW_CHUNKS == 8, "staging covers wave tiles 128 or 64 columns wide");
+        static_assert(W * WTM * ROW_BYTES <= LDS_BYTES, "the waves' tiles must fit the LDS ring");
+        unsigned char* stage = lds + wave * WTM * ROW_BYTES;
+#pragma unroll
+        for (int i = 0; i < FM; ++i) {
+            const int r = 16 * i + l16;
+#pragma unroll
+            for (int j = 0; j < FN; ++j) {
+                const f32x4& v = acc[i][j];
+                u32x2 packed;
+                if constexpr (SCALED) packed = pack4<DT>(v[0] * alpha, v[1] * alpha, v[2] * alpha, v[3] * alpha);
+                else packed = pack4<DT>(v[0], v[1], v[2], v[3]);
+                const int chunk = (2 * j + (g >> 1)) ^ (r % ROW_CHUNKS);
+                *reinterpret_cast<u32x2*>(stage + r * ROW_BYTES + chunk * 16 + 8 * (g & 1)) = packed;
+            }
+        }
+        store_staged_tile<WTM, ROW_BYTES>(stage, C, M, N, tm * BM + wm * WTM, (int64_t)tn * BN + wn * WTN, lane);
+    } else {
+        float* part = ws + (int64_t)split * M * N;
+        const int row0 = tm * BM + wm * WTM + l16;
+        const int64_t col0 = (int64_t)tn * BN + wn * WTN + 4 * g;
+#pragma unroll
+        for (int i = 0; i < FM; ++i) {
+            if (row0 + 16 * i >= M) continue;
+            float* prow = part + (int64_t)(row0 + 16 * i) * N;
+#pragma unroll
+            for (int j = 0; j < FN; ++j) *reinterpret_cast<f32x4*>(prow + col0 + 16 * j) = acc[i][j];
         }
     }
 }
@@ -596,15 +977,20 @@ int launch_cfg(const void* A, const void* B, void* C, int64_t M, int64_t N, int6
     const auto* b = static_cast<const unsigned char*>(B);
     auto* cp = static_cast<unsigned char*>(C);
     // Only fp8 carries a scale; the split-K partials are scaled by the reduction.
-    if (is_fp8(DT) && alpha != 1.0f && splits == 1) {
-        hipLaunchKernelGGL((gemm_tiled_kernel<DT, c.bm, c.bn, c.wgm, c.wgn, c.na, c.nb, is_fp8(DT)>), grid, block, 0,
-                           stream, a, b, cp, (int)M, (int)N, (int)K, alpha, tiles_m, tiles_n, c.group_m, splits,
-                           (int)(K / splits), ws);
-    } else {
-        hipLaunchKernelGGL((gemm_tiled_kernel<DT, c.bm, c.bn, c.wgm, c.wgn, c.na, c.nb, false>), grid, block, 0,
-                           stream, a, b, cp, (int)M, (int)N, (int)K, 1.0f, tiles_m, tiles_n, c.group_m, splits,
-                           (int)(K / splits), ws);
+    // fp8 runs the 16x16x128 kernel when the plan says so (frag_m 16).
+    typedef void (*Kernel)(const unsigned char*, const unsigned char*, unsigned char*, int, int, int, float, int,
+                           int, int, int, int, float*);
+    const bool scaled = is_fp8(DT) && alpha != 1.0f && splits == 1;
+    Kernel kernel = gemm_tiled_kernel<DT, c.bm, c.bn, c.wgm, c.wgn, c.na, c.nb, false>;
+    if constexpr (is_fp8(DT)) {
+        if (plan.frag_m == 16)
+            kernel = scaled ? gemm_fp8_mi16_kernel<DT, c.bm, c.bn, c.wgm, c.wgn, c.na, c.nb, true>
+                            : gemm_fp8_mi16_kernel<DT, c.bm, c.bn, c.wgm, c.wgn, c.na, c.nb, false>;
+        else if (scaled)
+            kernel = gemm_tiled_kernel<DT, c.bm, c.bn, c.wgm, c.wgn, c.na, c.nb, true>;
     }
+    hipLaunchKernelGGL(kernel, grid, block, 0, stream, a, b, cp, (int)M, (int)N, (int)K, scaled ? alpha : 1.0f,
+                       tiles_m, tiles_n, c.group_m, splits, (int)(K / splits), ws);
     MB_HIP_TRY(hipGetLastError());
     if (splits > 1) {
         const int64_t quads = M * N / 4;
@@ -708,7 +1094,18 @@ int gemm_tiled_plan(int dtype, int64_t M, int64_t N, int64_t K, const DeviceProp
     }
     if (tiles(cfg) * splits > INT32_MAX) return MB_ERR_SHAPE;
     const TiledConfig& c = kConfigs[cfg];
-    plan->implementation = "gfx950_mfma32_lds_dma";
+    // fp8 takes v_mfma_scale_f32_16x16x128_f8f6f4 on the 256 x 256 and
+    // 128 x 256 tiles when every split holds an even number of stages (one
+    // MFMA spans two): 2.3-4.2% faster than the 32x32x64 kernel on MI355X at
+    // 4096^3-16384^3, equal at 8192 x 1024 x 8192. On 128 x 128 tiles (eight
+    // MFMAs per step) it ran 2-4% slower, so those keep 32x32x64.
+    // MB_GEMM_FP8_MFMA=16 or 32 forces either (tuning/testing override).
+    const char* fp8_mfma = std::getenv("MB_GEMM_FP8_MFMA");
+    const int mfma_force = fp8_mfma != nullptr && *fp8_mfma != '\0' ? std::atoi(fp8_mfma) : 0;
+    const bool mi16 = e == 1 && (K / splits) % (2 * stage_k) == 0 &&
+                      (mfma_force == 16 || (mfma_force != 32 && cfg != 2));
+    const int frag = mi16 ? 16 : 32;
+    plan->implementation = mi16 ? "gfx950_mfma16_lds_dma" : "gfx950_mfma32_lds_dma";
     plan->threads = 64 * c.wgm * c.wgn;
     plan->grid = (int)(tiles(cfg) * splits);
     plan->tile_m = c.bm;
@@ -716,11 +1113,11 @@ int gemm_tiled_plan(int dtype, int64_t M, int64_t N, int64_t K, const DeviceProp
     plan->tile_k = (int)stage_k;
     plan->wave_grid_m = c.wgm;
     plan->wave_grid_n = c.wgn;
-    plan->wave_tile_m = c.bm / c.wgm / 32;
-    plan->wave_tile_n = c.bn / c.wgn / 32;
-    plan->frag_m = 32;
-    plan->frag_n = 32;
-    plan->frag_k = is_fp8(dtype) ? 64 : 16;
+    plan->wave_tile_m = c.bm / c.wgm / frag;
+    plan->wave_tile_n = c.bn / c.wgn / frag;
+    plan->frag_m = frag;
+    plan->frag_n = frag;
+    plan->frag_k = mi16 ? 128 : is_fp8(dtype) ? 64 : 16;
     plan->k_stages = c.nb;
     plan->split_k = splits;
     plan->tile_group_m = c.group_m;

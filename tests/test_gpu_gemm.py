@@ -11,7 +11,10 @@ where the fp32 accumulation is exact.
 """
 from __future__ import annotations
 
+import os
+
 import numpy as np
+
 import pytest
 import torch
 
@@ -31,6 +34,18 @@ HIGHP = ["float32", "float64"]
 # unit roundoff of the accumulation type
 UNIT = {"float32": 2.0**-24, "float64": 2.0**-53}
 
+
+
+def tiled_impl(dtype: str, k: int, info: dict) -> str:
+    """The tiled kernel a plan takes: fp8 runs v_mfma_scale_f32_16x16x128_f8f6f4 on 256 x 256 and
+    128 x 256 tiles when every split holds an even number of 64-byte stages, the 32x32 kernels
+    otherwise (MB_GEMM_FP8_MFMA=16 / 32 force either)."""
+    force = os.environ.get("MB_GEMM_FP8_MFMA", "")
+    big_tile = (info["tile_m"], info["tile_n"]) != (128, 128)
+    if dtype.startswith("float8") and (k // info["split_k"]) % 128 == 0 and \
+            (force == "16" or (force != "32" and big_tile)):
+        return "gfx950_mfma16_lds_dma"
+    return "gfx950_mfma32_lds_dma"
 
 def _gemm(lib, dtype: str, a: torch.Tensor, b: torch.Tensor, sa: float = 1.0, sb: float = 1.0) -> torch.Tensor:
     m, k = a.shape
@@ -76,7 +91,7 @@ def test_tiled_configurations(lib, dtype, config, shape, monkeypatch):
     monkeypatch.setenv("MB_GEMM_TILED_CONFIG", config)
     m, n, k = shape
     info = lib.gemm_info(capi.DTYPES[dtype], m, n, k)
-    assert info["implementation"] == "gfx950_mfma32_lds_dma"
+    assert info["implementation"] == tiled_impl(dtype, k, info)
     assert (info["tile_m"], info["tile_n"]) == {"0": (256, 256), "1": (128, 256), "2": (128, 128)}[config]
     print(f"[gemm] tiled cfg {config} {dtype} {shape}", flush=True)
     _check_random(lib, dtype, m, n, k, seed=k)
@@ -94,7 +109,7 @@ def test_tiled_stage_counts(lib, dtype, config, ksteps, monkeypatch):
     k = ksteps * (64 if dtype.startswith("float8") else 32)
     m, n = 300, 512
     info = lib.gemm_info(capi.DTYPES[dtype], m, n, k)
-    assert info["implementation"] == "gfx950_mfma32_lds_dma" and info["split_k"] == 1
+    assert info["implementation"] == tiled_impl(dtype, k, info) and info["split_k"] == 1
     print(f"[gemm] stages {ksteps} cfg {config} {dtype} {m}x{n}x{k}", flush=True)
     _check_random(lib, dtype, m, n, k, seed=ksteps)
 
@@ -107,7 +122,7 @@ def test_forced_splits_with_odd_stage_counts(lib, dtype, splits, ksteps, monkeyp
     k = ksteps * (64 if dtype.startswith("float8") else 32)
     m, n = 128, 512
     info = lib.gemm_info(capi.DTYPES[dtype], m, n, k)
-    assert info["implementation"] == "gfx950_mfma32_lds_dma" and info["split_k"] == splits
+    assert info["implementation"] == tiled_impl(dtype, k, info) and info["split_k"] == splits
     print(f"[gemm] splits {splits} x {ksteps // splits} stages {dtype} {m}x{n}x{k}", flush=True)
     _check_random(lib, dtype, m, n, k, seed=splits)
 
@@ -120,7 +135,7 @@ def test_n_multiple_of_128_takes_128x128_tiles(lib, dtype, shape, monkeypatch):
     monkeypatch.setenv("MB_GEMM_NO_GEMV", "1")  # keep M <= 4 on the tiled kernel too
     m, n, k = shape
     info = lib.gemm_info(capi.DTYPES[dtype], m, n, k)
-    assert info["implementation"] == "gfx950_mfma32_lds_dma" and (info["tile_m"], info["tile_n"]) == (128, 128)
+    assert info["implementation"] == tiled_impl(dtype, k, info) and (info["tile_m"], info["tile_n"]) == (128, 128)
     print(f"[gemm] n%128 {dtype} {shape} split {info['split_k']}", flush=True)
     _check_random(lib, dtype, m, n, k, seed=n + 3)
 
@@ -167,7 +182,7 @@ def test_skinny_shapes_split_k(lib, dtype, shape):
     info = lib.gemm_info(capi.DTYPES[dtype], m, n, k)
     splits = info["split_k"]
     # M <= 4 with 16-bit inputs streams B through the small-M kernel instead
-    expect = "gfx950_gemv_stream" if m <= 4 and dtype in ("bfloat16", "float16") else "gfx950_mfma32_lds_dma"
+    expect = "gfx950_gemv_stream" if m <= 4 and dtype in ("bfloat16", "float16") else tiled_impl(dtype, k, info)
     assert info["implementation"] == expect and splits >= 2
     assert info["workspace_bytes"] == splits * m * n * 4
     print(f"[gemm] skinny {dtype} {shape} split {splits}", flush=True)
@@ -205,7 +220,7 @@ def test_workspace_too_small_is_rejected(lib):
 def test_large_square_takes_the_big_tile(lib, dtype):
     m = n = k = 4096
     info = lib.gemm_info(capi.DTYPES[dtype], m, n, k)
-    assert info["tile_m"] == 256 and info["implementation"] == "gfx950_mfma32_lds_dma"
+    assert info["tile_m"] == 256 and info["implementation"] == tiled_impl(dtype, k, info)
     print(f"[gemm] {dtype} 4096^3 (rows sampled)", flush=True)
     _check_random(lib, dtype, m, n, k, rows=512)
 
@@ -450,3 +465,79 @@ def test_small_m_one_split_writes_c_directly(lib):
     m, n, k = 2, 65544, 64
     info = lib.gemm_info(capi.DT_BFLOAT16, m, n, k)
     assert info["split_k"] == 1 and info["workspace_bytes"] == 0
+
+
+@pytest.mark.parametrize("dtype", ["bfloat16", "float8_e4m3fn"])
+@pytest.mark.parametrize("config, splits", [("1", 4), ("2", 2), ("2", 8)])
+def test_split_k_reduction_ignores_workspace_contents(lib, dtype, config, splits, monkeypatch):
+    # The caller's workspace is never cleared: every split writes its whole fp32 partial before the
+    # reduction reads it, so whatever the workspace held (0xFF bytes, random bytes, zeros, the same
+    # call's partials, another shape's partials), the split-K result must be the same, bit for bit.
+    monkeypatch.setenv("MB_GEMM_TILED_CONFIG", config)
+    monkeypatch.setenv("MB_GEMM_SPLITS", str(splits))
+    m, n, k = 100, 1024, 64 * 8 * splits
+    dt = capi.DTYPES[dtype]
+    info = lib.gemm_info(dt, m, n, k)
+    assert info["split_k"] == splits
+    ops = rp.gemm_inputs(m, n, k, dtype, seed=splits)
+    a, b = ops["a"].cuda(), ops["b"].cuda()
+    ws_bytes = lib.gemm_workspace_size(dt, m, n, k)
+    stream = torch.cuda.current_stream().cuda_stream
+
+    def run(ws):
+        c = torch.full((m, n), float("nan"), dtype=rp.gemm_output_dtype(dtype), device="cuda")
+        lib.gemm(dt, a.data_ptr(), b.data_ptr(), c.data_ptr(), m, n, k, ops["scale_a"], ops["scale_b"],
+                 ws.data_ptr(), ws_bytes, stream)
+        torch.cuda.synchronize()
+        return c.cpu()
+
+    gen = torch.Generator(device="cuda").manual_seed(1)
+    ws = torch.full((ws_bytes,), 0xFF, dtype=torch.uint8, device="cuda")
+    print(f"[gemm] split-K workspace contents {dtype} cfg {config} splits {splits}", flush=True)
+    first = run(ws)
+    results = [run(ws)]                                                     # the same call's counters
+    results.append(run(torch.randint(0, 256, (ws_bytes,), dtype=torch.uint8, device="cuda", generator=gen)))
+    results.append(run(torch.zeros(ws_bytes, dtype=torch.uint8, device="cuda")))
+    # another shape through the same workspace, then this one again
+    m2, n2, k2 = 37, 512, 64 * 4 * splits
+    ops2 = rp.gemm_inputs(m2, n2, k2, dtype, seed=7)
+    c2 = torch.empty((m2, n2), dtype=rp.gemm_output_dtype(dtype), device="cuda")
+    assert lib.gemm_workspace_size(dt, m2, n2, k2) <= ws_bytes
+    lib.gemm(dt, ops2["a"].cuda().data_ptr(), ops2["b"].cuda().data_ptr(), c2.data_ptr(), m2, n2, k2,
+             ops2["scale_a"], ops2["scale_b"], ws.data_ptr(), ws_bytes, stream)
+    results.append(run(ws))
+    for r in results:
+        assert rp.bits_equal(r, first)
+    ref = rp.gemm_reference(ops["a"], ops["b"], ops["scale_a"], ops["scale_b"])
+    assert rp.rel_frobenius(first.float(), ref) <= REL_FROB[dtype]
+
+
+@pytest.mark.parametrize("dtype", ["float8_e4m3fn", "float8_e5m2"])
+@pytest.mark.parametrize("config, shape", [("0", (512, 512, 1024)), ("1", (384, 768, 640)), ("2", (200, 384, 1152)),
+                                           ("0", (256, 256, 128))])
+def test_fp8_16x16_and_32x32_kernels_agree(lib, dtype, config, shape, monkeypatch):
+    # The 16x16x128 kernel and the 32x32x64 one (MB_GEMM_FP8_MFMA=32) on the same inputs: both within
+    # the fp8 tolerance of the fp32 reference, and within fp32 summation-order noise of each other.
+    monkeypatch.setenv("MB_GEMM_TILED_CONFIG", config)
+    monkeypatch.setenv("MB_GEMM_SPLITS", "1")
+    m, n, k = shape
+    dt = capi.DTYPES[dtype]
+    ops = rp.gemm_inputs(m, n, k, dtype, seed=k)
+    a, b = ops["a"].cuda(), ops["b"].cuda()
+    out = {}
+    for mfma in ("16", "32"):
+        monkeypatch.setenv("MB_GEMM_FP8_MFMA", mfma)
+        info = lib.gemm_info(dt, m, n, k)
+        assert info["implementation"] == f"gfx950_mfma{mfma}_lds_dma" and info["frag_m"] == int(mfma)
+        c = torch.full((m, n), float("nan"), dtype=rp.gemm_output_dtype(dtype), device="cuda")
+        lib.gemm(dt, a.data_ptr(), b.data_ptr(), c.data_ptr(), m, n, k, ops["scale_a"], ops["scale_b"], 0, 0,
+                 torch.cuda.current_stream().cuda_stream)
+        torch.cuda.synchronize()
+        out[mfma] = c.cpu().float()
+    print(f"[gemm] fp8 16x16 vs 32x32 {dtype} cfg {config} {shape}", flush=True)
+    ref = rp.gemm_reference(ops["a"], ops["b"], ops["scale_a"], ops["scale_b"])
+    for c in out.values():
+        assert torch.isfinite(c).all()
+        assert rp.rel_frobenius(c, ref) <= REL_FROB[dtype]
+    # the two differ only by fp32 summation order before the bf16 rounding: a few bf16 ulps at most
+    assert rp.rel_frobenius(out["16"], out["32"]) <= 1e-2
