@@ -1036,6 +1036,19 @@ int gemm_tiled_plan(int dtype, int64_t M, int64_t N, int64_t K, const DeviceProp
     if (n128_only) cfg = 2;
     const bool forced = cfg >= 0;
     if (cfg < 0) cfg = (tiles(0) >= cus && M % kConfigs[0].bm == 0) ? 0 : 1;
+    // Last-round fill. 128 x 256 tiles run 7-14% below 256 x 256 per FLOP on
+    // MI355X, and a partly filled last round costs less than a full one (the
+    // busy CUs clock up under the power limit), so the smaller tile pays only
+    // when the last 256 x 256 round is at most a quarter full and there are
+    // few rounds: 2560 x 8192 x 8192 ran 11-14% faster on 128 x 256 tiles,
+    // 6144^3 1-5%, while 2.5- and 3.5-round shapes ran 3-15% slower.
+    // Such shapes have at least one tile per CU: no K split.
+    bool fill_rule = false;
+    if (!forced && cfg == 0) {
+        const int64_t full = tiles(0) / cus, rest = tiles(0) % cus;
+        fill_rule = full <= 2 && rest > 0 && 4 * rest <= cus;
+        if (fill_rule) cfg = 1;
+    }
     // K splits for problems with too few tiles to fill the GPU, chosen by a
     // cost model whose four constants were fitted to a sweep on MI355X (bf16
     // and fp8 e4m3; M = 16..8192, N = 1024..16384, K = 2048..16384; every
@@ -1060,7 +1073,7 @@ int gemm_tiled_plan(int dtype, int64_t M, int64_t N, int64_t K, const DeviceProp
     // 4096 by 21%, 256 x 512 x 1024 by 34%) and 12 of 13 fp8 shapes (up to
     // 30%; 16 x 8192 x 8192 fp8 5% slower).
     int splits = 1;
-    if (kConfigs[cfg].bm == 128) {
+    if (kConfigs[cfg].bm == 128 && !fill_rule) {
         const int cands[2] = {cfg, 2};
         const int n_cands = (!forced && cfg == 1) ? 2 : 1;
         const double flops_per_cu = 6.0e12 * (e == 1 ? 2.0 : 1.0), bw = 5.0e12;

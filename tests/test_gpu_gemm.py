@@ -541,3 +541,15 @@ def test_fp8_16x16_and_32x32_kernels_agree(lib, dtype, config, shape, monkeypatc
         assert rp.rel_frobenius(c, ref) <= REL_FROB[dtype]
     # the two differ only by fp32 summation order before the bf16 rounding: a few bf16 ulps at most
     assert rp.rel_frobenius(out["16"], out["32"]) <= 1e-2
+
+
+@pytest.mark.parametrize("dtype", ["bfloat16", "float8_e4m3fn"])
+@pytest.mark.parametrize("shape, tile_m", [((2560, 8192, 8192), 128), ((6144, 6144, 6144), 128),
+                                           ((4096, 14336, 4096), 256), ((5120, 5120, 5120), 256),
+                                           ((8192, 8192, 8192), 256), ((7168, 7168, 7168), 256)])
+def test_mostly_empty_last_round_takes_128_row_tiles(lib, dtype, shape, tile_m):
+    # 256 x 256 tiles leave a last round at most a quarter full (and at most two full rounds before it)
+    # only for the first two shapes; those take 128 x 256 tiles.
+    m, n, k = shape
+    info = lib.gemm_info(capi.DTYPES[dtype], m, n, k)
+    assert (info["tile_m"], info["tile_n"], info["split_k"]) == (tile_m, 256, 1)
