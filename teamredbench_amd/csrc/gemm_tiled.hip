@@ -264,7 +264,7 @@ __device__ __forceinline__ void store_staged_tile(const unsigned char* stage, un
     const int64_t ldc = (int64_t)N * 2;  // bytes per C row (16-bit output)
     constexpr int ROWS_PER_STORE = 64 / ROW_CHUNKS;
     constexpr int STORES = WTM / ROWS_PER_STORE;
-    constexpr int BATCH = 8;
+    constexpr int BATCH = STORES < 8 ? STORES : 8;
     static_assert(STORES % BATCH == 0, "stores split into batches");
     const int c = lane % ROW_CHUNKS;
     const int r0 = lane / ROW_CHUNKS;
@@ -962,6 +962,7 @@ constexpr TiledConfig kConfigs[] = {
     {256, 256, 2, 2, 3, 4, 4},  // 0: large problems, 128 x 128 per wave; 3 x 32 + 4 x 16 KiB
     {128, 256, 2, 2, 3, 6, 8},  // 1: mid-size problems, 64 x 128 per wave; 3 x 16 + 6 x 16 KiB
     {128, 128, 2, 2, 3, 6, 4},  // 2: few tiles, N % 256 != 0: 64 x 64 per wave; 3 x 16 + 6 x 8 KiB
+    {64, 128, 2, 2, 3, 6, 4},   // 3: small and skinny problems: 32 x 64 per wave; 3 x 8 + 6 x 8 KiB
 };
 constexpr int kNumConfigs = sizeof(kConfigs) / sizeof(kConfigs[0]);
 
@@ -1007,6 +1008,7 @@ int launch_dtype(const GemmPlan& plan, const void* A, const void* B, void* C, in
                  float alpha, void* workspace, hipStream_t stream) {
     if (plan.config == 0) return launch_cfg<DT, 0>(A, B, C, M, N, K, alpha, plan, workspace, stream);
     if (plan.config == 2) return launch_cfg<DT, 2>(A, B, C, M, N, K, alpha, plan, workspace, stream);
+    if (plan.config == 3) return launch_cfg<DT, 3>(A, B, C, M, N, K, alpha, plan, workspace, stream);
     return launch_cfg<DT, 1>(A, B, C, M, N, K, alpha, plan, workspace, stream);
 }
 
@@ -1033,7 +1035,8 @@ int gemm_tiled_plan(int dtype, int64_t M, int64_t N, int64_t K, const DeviceProp
         const int f = std::atoi(force);
         if (f >= 0 && f < kNumConfigs) cfg = f;
     }
-    if (n128_only) cfg = 2;
+    const bool env_forced = cfg >= 0;
+    if (n128_only && cfg != 3) cfg = 2;
     const bool forced = cfg >= 0;
     if (cfg < 0) cfg = (tiles(0) >= cus && M % kConfigs[0].bm == 0) ? 0 : 1;
     // Last-round fill. 128 x 256 tiles run 7-14% below 256 x 256 per FLOP on
@@ -1100,6 +1103,13 @@ int gemm_tiled_plan(int dtype, int64_t M, int64_t N, int64_t K, const DeviceProp
         }
         cfg = best_cfg;
     }
+    // 64 x 128 tiles for problems the 128 x 128 plan leaves with few blocks:
+    // at the same split count they halve each block's MFMA work and double
+    // the blocks. Taken when the doubled count still fits in half the CUs:
+    // on MI355X 1024^3 ran 22% faster, 640 x 1536 x 768 19%, 100 x 2048 x 4096
+    // 17%, 512 x 256 x 4096 15% (bf16 and fp8 alike); with more blocks than
+    // that the narrower tile lost (3072^3 7-11% slower).
+    if (!env_forced && cfg == 2 && tiles(3) * splits * 2 <= cus) cfg = 3;
     const char* force_splits = std::getenv("MB_GEMM_SPLITS");  // tuning/testing override
     if (force_splits != nullptr && *force_splits != '\0') {
         const int f = std::atoi(force_splits);
@@ -1116,7 +1126,7 @@ int gemm_tiled_plan(int dtype, int64_t M, int64_t N, int64_t K, const DeviceProp
     const char* fp8_mfma = std::getenv("MB_GEMM_FP8_MFMA");
     const int mfma_force = fp8_mfma != nullptr && *fp8_mfma != '\0' ? std::atoi(fp8_mfma) : 0;
     const bool mi16 = e == 1 && (K / splits) % (2 * stage_k) == 0 &&
-                      (mfma_force == 16 || (mfma_force != 32 && cfg != 2));
+                      (mfma_force == 16 || (mfma_force != 32 && c.bn == 256));
     const int frag = mi16 ? 16 : 32;
     plan->implementation = mi16 ? "gfx950_mfma16_lds_dma" : "gfx950_mfma32_lds_dma";
     plan->threads = 64 * c.wgm * c.wgn;

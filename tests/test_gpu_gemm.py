@@ -41,7 +41,7 @@ def tiled_impl(dtype: str, k: int, info: dict) -> str:
     128 x 256 tiles when every split holds an even number of 64-byte stages, the 32x32 kernels
     otherwise (MB_GEMM_FP8_MFMA=16 / 32 force either)."""
     force = os.environ.get("MB_GEMM_FP8_MFMA", "")
-    big_tile = (info["tile_m"], info["tile_n"]) != (128, 128)
+    big_tile = info["tile_n"] == 256
     if dtype.startswith("float8") and (k // info["split_k"]) % 128 == 0 and \
             (force == "16" or (force != "32" and big_tile)):
         return "gfx950_mfma16_lds_dma"
@@ -83,7 +83,7 @@ def test_gemm_random_matches_fp32_matmul(lib, dtype, shape):
 
 
 @pytest.mark.parametrize("dtype", LOWP)
-@pytest.mark.parametrize("config", ["0", "1", "2"])
+@pytest.mark.parametrize("config", ["0", "1", "2", "3"])
 @pytest.mark.parametrize("shape", [(256, 256, 128), (256, 512, 64), (256, 512, 1024), (512, 256, 4096), (768, 1280, 384)])
 def test_tiled_configurations(lib, dtype, config, shape, monkeypatch):
     # Every tiled configuration on shapes it divides, selected through the
@@ -92,13 +92,13 @@ def test_tiled_configurations(lib, dtype, config, shape, monkeypatch):
     m, n, k = shape
     info = lib.gemm_info(capi.DTYPES[dtype], m, n, k)
     assert info["implementation"] == tiled_impl(dtype, k, info)
-    assert (info["tile_m"], info["tile_n"]) == {"0": (256, 256), "1": (128, 256), "2": (128, 128)}[config]
+    assert (info["tile_m"], info["tile_n"]) == {"0": (256, 256), "1": (128, 256), "2": (128, 128), "3": (64, 128)}[config]
     print(f"[gemm] tiled cfg {config} {dtype} {shape}", flush=True)
     _check_random(lib, dtype, m, n, k, seed=k)
 
 
 @pytest.mark.parametrize("dtype", ["bfloat16", "float8_e4m3fn"])
-@pytest.mark.parametrize("config", ["0", "1", "2"])
+@pytest.mark.parametrize("config", ["0", "1", "2", "3"])
 @pytest.mark.parametrize("ksteps", [1, 2, 3, 4, 5, 6, 7, 8, 9, 11, 12, 13, 25, 37])
 def test_tiled_stage_counts(lib, dtype, config, ksteps, monkeypatch):
     # A is loaded two 64-byte K stages at a time: odd stage counts leave the
@@ -135,32 +135,34 @@ def test_n_multiple_of_128_takes_128x128_tiles(lib, dtype, shape, monkeypatch):
     monkeypatch.setenv("MB_GEMM_NO_GEMV", "1")  # keep M <= 4 on the tiled kernel too
     m, n, k = shape
     info = lib.gemm_info(capi.DTYPES[dtype], m, n, k)
-    assert info["implementation"] == tiled_impl(dtype, k, info) and (info["tile_m"], info["tile_n"]) == (128, 128)
+    assert info["implementation"] == tiled_impl(dtype, k, info) and info["tile_n"] == 128 and info["tile_m"] in (64, 128)
     print(f"[gemm] n%128 {dtype} {shape} split {info['split_k']}", flush=True)
     _check_random(lib, dtype, m, n, k, seed=n + 3)
 
 
 @pytest.mark.parametrize("dtype", ["bfloat16", "float16"])
-@pytest.mark.parametrize("shape", [(2048, 2048, 2048), (1024, 1024, 1024), (640, 1536, 768)])
-def test_few_tiles_take_128x128_tiles(lib, dtype, shape):
+@pytest.mark.parametrize("shape, tile_m", [((2048, 2048, 2048), 128), ((1024, 1024, 1024), 64), ((640, 1536, 768), 64)])
+def test_few_tiles_take_128x128_tiles(lib, dtype, shape, tile_m):
     # Several tile rows that would leave half the CUs idle on 128 x 256 tiles
-    # run 128 x 128 tiles, unsplit (the default plan, not an override).
+    # run 128 x 128 tiles, unsplit (the default plan, not an override); when
+    # twice their block count still fits in half the CUs, 64 x 128 tiles.
     m, n, k = shape
     info = lib.gemm_info(capi.DTYPES[dtype], m, n, k)
-    assert (info["tile_m"], info["tile_n"], info["split_k"]) == (128, 128, 1)
+    assert (info["tile_m"], info["tile_n"], info["split_k"]) == (tile_m, 128, 1)
     print(f"[gemm] 128x128 default {dtype} {shape}", flush=True)
     _check_random(lib, dtype, m, n, k, seed=n)
 
 
 @pytest.mark.parametrize("dtype", ["bfloat16", "float16"])
-@pytest.mark.parametrize("shape", [(16, 8192, 8192), (128, 8192, 8192)])
-def test_skinny_benchmark_shapes_split_two_ways_on_128x128_tiles(lib, dtype, shape):
+@pytest.mark.parametrize("shape, tile_m", [((16, 8192, 8192), 64), ((128, 8192, 8192), 128)])
+def test_skinny_benchmark_shapes_split_two_ways_on_128x128_tiles(lib, dtype, shape, tile_m):
     # The split-K cost model's pick for the two skinny benchmark shapes with 16-bit inputs: 2 splits over
     # 128 x 128 tiles (measured 24.7 / 31.4 us against 25.9 / 32.2 for 4 splits over 128 x 256 tiles, and
-    # 31 / 45 us for the 16 / 8 splits a tile-count rule picks).
+    # 31 / 45 us for the 16 / 8 splits a tile-count rule picks); at 16 rows the 128 blocks fit in half
+    # the CUs on 64 x 128 tiles too, which take them.
     m, n, k = shape
     info = lib.gemm_info(capi.DTYPES[dtype], m, n, k)
-    assert (info["tile_m"], info["tile_n"], info["split_k"]) == (128, 128, 2)
+    assert (info["tile_m"], info["tile_n"], info["split_k"]) == (tile_m, 128, 2)
     assert lib.gemm_workspace_size(capi.DTYPES[dtype], m, n, k) == 2 * m * n * 4
     _check_random(lib, dtype, m, n, k, seed=m, rows=64)
 
@@ -514,7 +516,7 @@ def test_split_k_reduction_ignores_workspace_contents(lib, dtype, config, splits
 
 @pytest.mark.parametrize("dtype", ["float8_e4m3fn", "float8_e5m2"])
 @pytest.mark.parametrize("config, shape", [("0", (512, 512, 1024)), ("1", (384, 768, 640)), ("2", (200, 384, 1152)),
-                                           ("0", (256, 256, 128))])
+                                           ("0", (256, 256, 128)), ("3", (136, 384, 1024))])
 def test_fp8_16x16_and_32x32_kernels_agree(lib, dtype, config, shape, monkeypatch):
     # The 16x16x128 kernel and the 32x32x64 one (MB_GEMM_FP8_MFMA=32) on the same inputs: both within
     # the fp8 tolerance of the fp32 reference, and within fp32 summation-order noise of each other.

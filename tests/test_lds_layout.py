@@ -111,7 +111,7 @@ def test_b_transposing_reads_are_conflict_free():
                 assert worst_lanes_per_bank(addrs, 8, 32, 64) == 1
 
 
-@pytest.mark.parametrize("bm, waves", [(256, 4), (128, 4)])
+@pytest.mark.parametrize("bm, waves", [(256, 4), (128, 4), (64, 4)])
 @pytest.mark.parametrize("lda", [128, 8192, 16384 + 128])  # A row bytes, multiples of 128
 def test_a_loads_cover_whole_lines_and_split_offsets(bm, waves, lda):
     pair_bytes = 2 * bm * STAGE
@@ -206,8 +206,8 @@ def simulate_ring(na: int, nb: int, ai: int, bi: int, ksteps: int,
 
 
 # (A pair slots, B stage slots, A loads per wave per pair, B loads per wave per stage) of the
-# three tiled configurations: 256x256 (16-bit and fp8), 128x256, 128x128 (16-bit).
-CONFIGS = [(3, 4, 8, 4), (3, 6, 4, 4), (3, 6, 4, 2)]
+# four tiled configurations: 256x256 (16-bit and fp8), 128x256, 128x128 and 64x128 (16-bit).
+CONFIGS = [(3, 4, 8, 4), (3, 6, 4, 4), (3, 6, 4, 2), (3, 6, 2, 2)]
 
 
 @pytest.mark.parametrize("cfg", CONFIGS)
@@ -221,6 +221,7 @@ def test_ring_waits_of_the_configurations():
     assert load_schedule(3, 4, 8, 4) == (28, 16, 16)
     assert load_schedule(3, 6, 4, 4) == (28, 20, 24)
     assert load_schedule(3, 6, 4, 2) == (18, 12, 16)
+    assert load_schedule(3, 6, 2, 2) == (14, 10, 12)
 
 
 @pytest.mark.parametrize("loosen", [(1, 0, 0), (0, 1, 0), (0, 0, 1)])
@@ -463,10 +464,10 @@ def simulate_ring_mi16(na: int, nb: int, ai: int, bi: int, ksteps: int,
 
 
 # (A pair slots, B stage slots, A loads per wave per pair, B loads per wave per stage): 256x256,
-# 128x256 and 128x128 tiles; steady-state waits allow the loads of the two previous steps pending.
-MI16_CONFIGS = [(3, 4, 8, 4), (3, 6, 4, 4), (3, 6, 4, 2)]
-MI16_WAITS = [(16, 16, 16), (16, 16, 20), (10, 10, 12)]
-MI16_WAITS_SPLIT_A = [(16, 12, 16), (12, 10, 16), (8, 6, 10)]
+# 128x256, 128x128 and 64x128 tiles; steady-state waits allow the loads of the two previous steps pending.
+MI16_CONFIGS = [(3, 4, 8, 4), (3, 6, 4, 4), (3, 6, 4, 2), (3, 6, 2, 2)]
+MI16_WAITS = [(16, 16, 16), (16, 16, 20), (10, 10, 12), (8, 8, 10)]
+MI16_WAITS_SPLIT_A = [(16, 12, 16), (12, 10, 16), (8, 6, 10), (6, 5, 8)]
 
 
 @pytest.mark.parametrize("split_a", [False, True])
