@@ -1,7 +1,7 @@
 // LDS-pipelined MFMA GEMM for gfx950: C = alpha * (A * B), A (M x K) and
 // B (K x N) row-major, fp32 accumulation, output bf16 (bf16 and fp8 e4m3 /
-// e5m2 inputs) or fp16 (fp16 inputs). Takes shapes with N % BN == 0 and K a
-// multiple of the stage depth, any M (the rows of a partial last M tile read
+// e5m2 inputs) or fp16 (fp16 inputs). Tiles of 256 x 256, 128 x 256, 128 x 128
+// or 64 x 128. Takes shapes with N % BN == 0 and K a multiple of the stage depth, any M (the rows of a partial last M tile read
 // as zeros and are not stored); everything else goes to the generic kernel.
 //
 // Data path. A stage is 64 bytes of K per row. A is held two stages at a
@@ -38,7 +38,9 @@
 //
 // Waves form a WGM x WGN grid; each wave owns (BM/WGM) x (BN/WGN) of C as
 // 32 x 32 fragments: v_mfma_f32_32x32x16_{bf16,f16} (two per stage), or for
-// fp8 v_mfma_f32_32x32x64_f8f6f4 (one per stage). The MFMA takes the B
+// fp8 v_mfma_f32_32x32x64_f8f6f4 (one per stage). fp8 on 256- and 128-row x
+// 256-column tiles runs gemm_fp8_mi16_kernel below instead: 16 x 16 fragments
+// on v_mfma_scale_f32_16x16x128_f8f6f4, one MFMA spanning a pair of stages. The MFMA takes the B
 // fragment as its first operand, so a lane's 16 accumulators are 4 runs of 4
 // consecutive C columns in one C row. The epilogue rounds them to 16 bits
 // through LDS so that the stores to C are whole 256-byte row segments.
