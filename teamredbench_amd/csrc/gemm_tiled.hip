@@ -1,8 +1,9 @@
 // LDS-pipelined MFMA GEMM for gfx950: C = alpha * (A * B), A (M x K) and
 // B (K x N) row-major, fp32 accumulation, output bf16 (bf16 and fp8 e4m3 /
-// e5m2 inputs) or fp16 (fp16 inputs). Tiles of 256 x 256, 128 x 256, 128 x 128
-// or 64 x 128. Takes shapes with N % BN == 0 and K a multiple of the stage depth, any M (the rows of a partial last M tile read
-// as zeros and are not stored); everything else goes to the generic kernel.
+// e5m2 inputs) or fp16 (fp16 inputs). Tiles of 256 x 256, 128 x 256,
+// 128 x 128 or 64 x 128. Takes shapes with N % BN == 0 and K a multiple of
+// the stage depth, any M (the rows of a partial last M tile read as zeros and
+// are not stored); everything else goes to the generic kernel.
 //
 // Data path. A stage is 64 bytes of K per row. A is held two stages at a
 // time, as [BM rows][128 B] pair slots; B one stage at a time, as
