@@ -1112,11 +1112,11 @@ int gemm_tiled_plan(int dtype, int64_t M, int64_t N, int64_t K, const DeviceProp
     // on MI355X 1024^3 ran 22% faster, 640 x 1536 x 768 19%, 100 x 2048 x 4096
     // 17%, 512 x 256 x 4096 15% (bf16 and fp8 alike); with more blocks than
     // that the narrower tile lost (3072^3 7-11% slower, 2048^3 27-55%), except
-    // for problems of one 128-row tile, up to one block per CU (128 x 8192 x
-    // 8192 at 2 splits: 4% bf16, 10% fp8).
-    if (!env_forced && cfg == 2 &&
-        (tiles(3) * splits * 2 <= cus || (M <= kConfigs[2].bm && tiles(3) * splits <= cus)))
-        cfg = 3;
+    // for bf16 and fp8 problems of one 128-row tile, up to one block per CU
+    // (128 x 8192 x 8192 at 2 splits: bf16 2.5-9.5%, fp8 9%; fp16 ran 4-7%
+    // slower at 128 x 8192 x 8192 and 128 x 4096 x 4096, so it keeps 128 x 128).
+    const bool one_tile_rule = dtype != MB_DT_FLOAT16 && M <= kConfigs[2].bm && tiles(3) * splits <= cus;
+    if (!env_forced && cfg == 2 && (tiles(3) * splits * 2 <= cus || one_tile_rule)) cfg = 3;
     const char* force_splits = std::getenv("MB_GEMM_SPLITS");  // tuning/testing override
     if (force_splits != nullptr && *force_splits != '\0') {
         const int f = std::atoi(force_splits);

@@ -153,13 +153,14 @@ def test_few_tiles_take_128x128_tiles(lib, dtype, shape, tile_m):
     _check_random(lib, dtype, m, n, k, seed=n)
 
 
-@pytest.mark.parametrize("dtype", ["bfloat16", "float16"])
-@pytest.mark.parametrize("shape, tile_m", [((16, 8192, 8192), 64), ((128, 8192, 8192), 64)])
+@pytest.mark.parametrize("dtype, shape, tile_m", [("bfloat16", (16, 8192, 8192), 64), ("float16", (16, 8192, 8192), 64),
+                                                  ("bfloat16", (128, 8192, 8192), 64),
+                                                  ("float16", (128, 8192, 8192), 128)])
 def test_skinny_benchmark_shapes_split_two_ways_on_128x128_tiles(lib, dtype, shape, tile_m):
     # The split-K cost model's pick for the two skinny benchmark shapes with 16-bit inputs: 2 splits over
     # 128 x 128 tiles (measured 24.7 / 31.4 us against 25.9 / 32.2 for 4 splits over 128 x 256 tiles, and
-    # 31 / 45 us for the 16 / 8 splits a tile-count rule picks); problems of one 128-row tile then take
-    # 64 x 128 tiles at the same split count while that is at most one block per CU.
+    # 31 / 45 us for the 16 / 8 splits a tile-count rule picks); 64 x 128 tiles then take the same
+    # split count when the blocks fit in half the CUs, or (bf16 and fp8) for one 128-row tile in all.
     m, n, k = shape
     info = lib.gemm_info(capi.DTYPES[dtype], m, n, k)
     assert (info["tile_m"], info["tile_n"], info["split_k"]) == (tile_m, 128, 2)
