@@ -15,11 +15,12 @@ in HBM. The printed JSON line carries:
   gemm                 bf16 and fp8 e4m3 GEMM TFLOPS and MFU at 8192^3
                        (event-timed, same library), with a sampled parity check;
   cpu_baseline         the reference torch op (torch.add(b, c, alpha=3.0,
-                       out=a)) on CPU tensors on this host's cores, timed over a
-                       bounded sample of the same workload.
+                       out=a)) on CPU tensors on this host's cores: the CPU
+                       triad configuration (2^24 elements, seed 0, 5 warmup +
+                       20 timed), plus the same op at the GPU step's size.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-gemm]
-                       [--cpu-seconds S]
+                       [--cpu-iterations I] [--no-cpu]
 """
 from __future__ import annotations
 
@@ -143,37 +144,61 @@ def bench_gemm(torch, lib, capi, dtype: str, size: int, warmup: int, iterations:
     }
 
 
-def cpu_baseline(seconds: float) -> dict:
-    """The reference torch op on CPU tensors (oracle restatement of hbm.py:29-39)."""
+def _cpu_quota() -> float | None:
+    """CPUs the cgroup quota allows this process (cpu.max), or None when unlimited or unreadable."""
+    try:
+        quota, period = Path("/sys/fs/cgroup/cpu.max").read_text(encoding="utf-8").split()[:2]
+        return None if quota == "max" else int(quota) / int(period)
+    except (OSError, ValueError):
+        return None
+
+
+def _time_triad_cpu(rp, n: int, warmup: int, iterations: int) -> float:
+    """Mean wall-clock seconds of torch.add(b, c, alpha=3.0, out=a) on CPU tensors, b then c drawn
+    uniform[-1, 1] fp32 from one generator seeded 0 (the reference path, hbm.py:36-38, timed as
+    utils.py:14-29 times it, without a device synchronisation)."""
+    import torch
+
+    b, c = rp.stream_inputs(n, "float32", seed=0)
+    a = torch.empty_like(b)
+    for _ in range(warmup):
+        rp.run_mode("triad", b, a, c, 3.0)
+    t0 = time.perf_counter()
+    for _ in range(iterations):
+        rp.run_mode("triad", b, a, c, 3.0)
+    return (time.perf_counter() - t0) / iterations
+
+
+def cpu_baseline(large_iterations: int) -> dict:
+    """The CPU triad configuration, timed as configured: 2^24 fp32 elements per array, seed 0, 5 warmup +
+    20 timed iterations, torch threads = every CPU this process may run on (sched_getaffinity), that
+    count recorded. The same op at the GPU step's 2^28 elements is reported beside it."""
     import torch
 
     from oracle import reference_path as rp
 
-    cores = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
-    cores = max(1, min(cores, 16))
+    cores = len(os.sched_getaffinity(0))
     torch.set_num_threads(cores)
-    n = TRIAD_ELEMENTS
-    b, c = rp.stream_inputs(n, "float32", seed=0)
-    a = torch.empty_like(b)
-    for _ in range(2):
-        rp.run_mode("triad", b, a, c, 3.0)
-    iters = 0
-    t0 = time.perf_counter()
-    while True:
-        rp.run_mode("triad", b, a, c, 3.0)
-        iters += 1
-        elapsed = time.perf_counter() - t0
-        if elapsed >= seconds:
-            break
-    per = elapsed / iters
-    return {
+    n = 1 << 24
+    per = _time_triad_cpu(rp, n, warmup=5, iterations=20)
+    out = {
         "value": 3 * 4 * n / per / 1e9,
         "unit": "GB/s",
         "cores": cores,
         "kind": "port",
-        "sample": (f"fp32 triad over 2^28 elements per array, torch.add(b, c, alpha=3.0, out=a) on CPU tensors, "
-                   f"{iters} iterations in {elapsed:.1f} s after 2 warmup"),
+        "sample": ("fp32 triad a = b + 3*c over 2^24 elements per array (b, c uniform[-1, 1] from seed 0), "
+                   "torch.add(b, c, alpha=3.0, out=a) on CPU tensors, 5 warmup + 20 timed iterations, "
+                   f"{per * 1e3:.3f} ms per iteration"),
+        "cpu_quota_cores": _cpu_quota(),
     }
+    if large_iterations > 0:
+        big = TRIAD_ELEMENTS
+        per_big = _time_triad_cpu(rp, big, warmup=2, iterations=large_iterations)
+        out["at_gpu_step_size"] = {
+            "value": 3 * 4 * big / per_big / 1e9, "unit": "GB/s", "elements": big,
+            "sample": f"the same op over 2^28 elements per array, 2 warmup + {large_iterations} timed iterations",
+        }
+    return out
 
 
 def main() -> int:
@@ -183,7 +208,10 @@ def main() -> int:
     parser.add_argument("--warmup", type=int, default=10)
     parser.add_argument("--no-gemm", action="store_true", help="skip the 8192^3 GEMM measurements")
     parser.add_argument("--gemm-iterations", type=int, default=50)
-    parser.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline sample length (0 = skip)")
+    parser.add_argument("--cpu-iterations", type=int, default=20,
+                        help="timed CPU iterations at the GPU step's 2^28 size, beside the 2^24 CPU triad "
+                             "configuration (0 = that configuration only); --no-cpu skips the CPU baseline")
+    parser.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     args = parser.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -218,9 +246,10 @@ def main() -> int:
             _log(f"gemm {dtype}: {gemm[dtype]['achieved_tflops']:.1f} TFLOPS ({gemm[dtype]['mfu_pct']:.1f}% MFU)")
 
     baseline = None
-    if args.cpu_seconds > 0:
-        _log(f"cpu baseline: {args.cpu_seconds:.0f} s sample")
-        baseline = cpu_baseline(args.cpu_seconds)
+    if not args.no_cpu:
+        _log("cpu baseline: 2^24 fp32 triad, 5 warmup + 20 timed")
+        baseline = cpu_baseline(args.cpu_iterations)
+        _log(f"cpu baseline: {baseline['value']:.1f} GB/s on {baseline['cores']} threads")
 
     traffic = read_traffic()
     line = {

@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define MB_ABI_VERSION 1
+#define MB_ABI_VERSION 2
 
 /* Status codes (negative = rejected by the library before any launch). */
 #define MB_OK 0
@@ -122,6 +122,7 @@ int mb_gemm(int dtype, const void* A, const void* B, void* C, int64_t M,
 /* Workspace bytes mb_gemm needs for this dtype and shape (0 if none). */
 size_t mb_gemm_workspace_size(int dtype, int64_t M, int64_t N, int64_t K);
 
+
 /*
  * mb_time_gemm -- warmup + event-timed loop of mb_gemm launches.
  *
@@ -143,10 +144,46 @@ int mb_time_gemm(int dtype, const void* A, const void* B, void* C, int64_t M,
  * wave_grid_*, wave_tile_*, frag_*, k_stages ...).
  * kind = MB_KIND_STREAM: a = op, b = dtype, m = n elements, n = blocks_per_cu.
  * kind = MB_KIND_GEMM:   a = dtype, m, n, k = shape (b ignored).
+ * Beyond the reference's keys: "overrides" (the MB_TUNE_* knobs in force,
+ * by name; {} normally) and, for GEMM, "workspace_bytes", "split_k" and
+ * "fallback" (why a faster kernel family could not take the shape and a
+ * bounds-checked kernel runs it instead; "" when none).
  * Returns MB_ERR_INVALID_ARG if json is NULL or cap is too small.
  */
 int mb_kernel_info(int kind, int a, int b, int64_t m, int64_t n, int64_t k,
                    char* json, size_t cap);
+
+/*
+ * Plan overrides. No counterpart in the reference, whose executables fix
+ * their tuning at compile time (hbm_bandwidth.hip.cpp:18-70,
+ * mfu_gemm_lowp.hip.hpp:7-37) apart from --blocks-per-cu (kept above as an
+ * argument of mb_stream). These knobs exist for tests and tuning sweeps that
+ * must run a specific kernel configuration. Each knob is process-wide and
+ * holds either -1 (the library's own choice, the default) or a forced value;
+ * nothing is read from the environment. mb_kernel_info reports every knob in
+ * force under "overrides", so a record shows when a non-default plan ran.
+ * Set knobs before the calls they should affect: a plan is made per call, so
+ * mb_gemm_workspace_size and mb_gemm must see the same settings.
+ */
+#define MB_TUNE_STREAM_UNROLL 0        /* 16-byte chunks per thread per trip: 1, 2, 4 or 8 */
+#define MB_TUNE_STREAM_NONTEMPORAL 1   /* 0 or 1: nontemporal loads and stores */
+#define MB_TUNE_STREAM_THREADS 2       /* threads per block: 64..1024, a multiple of 64 */
+#define MB_TUNE_STREAM_SCHEDULE 3      /* 0 grid-stride, 1 one contiguous span per block */
+#define MB_TUNE_GEMM_FORCE_GENERIC 4   /* 1: the bounds-checked generic kernel for 16-bit and fp8 */
+#define MB_TUNE_GEMM_NO_SMALL_M 5      /* 1: M <= 4 stays on the MFMA kernels */
+#define MB_TUNE_GEMM_TILED_CONFIG 6    /* 0: 256x256, 1: 128x256, 2: 128x128, 3: 64x128 tiles */
+#define MB_TUNE_GEMM_SPLITS 7          /* K splits, 1..64 (taken when the split K is whole stages) */
+#define MB_TUNE_GEMM_FP8_MFMA 8        /* 16 or 32: the fp8 MFMA shape on the tiled kernel */
+#define MB_TUNE_GEMM_HIGHP_STAGED 9    /* 1: fp32 / fp64 on the register-staged kernel */
+#define MB_TUNE_COUNT 10
+
+/* Force `knob` to `value`, or restore the library's choice with value -1.
+ * Returns MB_ERR_INVALID_ARG for an unknown knob or a value outside the
+ * range listed above. */
+int mb_set_tuning(int knob, int64_t value);
+
+/* The value `knob` holds (-1 = the library's choice); -1 for an unknown knob. */
+int64_t mb_get_tuning(int knob);
 
 /* Description of the last failure on the calling thread ("" if none). */
 const char* mb_last_error(void);

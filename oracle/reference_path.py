@@ -5,17 +5,13 @@ Follows, on CPU tensors:
   * src/teamredbench/benchmarks/hbm.py:29-39  _run_mode (copy_ / mul / add(alpha))
   * src/teamredbench/benchmarks/hbm.py:85,192 numel = size_mib * 2**20 // bytes
   * src/teamredbench/benchmarks/mfu.py:229-238 torch.mm(a, b, out=out)
-  * src/teamredbench/utils.py:14-29          timed_iterations (wall clock mean)
 The reference draws unseeded ``randn`` inputs (utils.py:32-48); the
-benchmark configurations this build measures fix seeded distributions
-instead, generated here with a CPU ``torch.Generator`` so the GPU and the CPU
+benchmark configurations measured here fix seeded distributions instead, generated here with a CPU ``torch.Generator`` so the GPU and the CPU
 see identical bits.
 """
 from __future__ import annotations
 
 import math
-import time
-from typing import Callable
 
 import numpy as np
 import torch
@@ -189,17 +185,6 @@ def max_abs_over_max_ref(out: torch.Tensor, ref: torch.Tensor) -> float:
     o = out.double()
     r = ref.double()
     return float((o - r).abs().max()) / max(float(r.abs().max()), 1e-12)
-
-
-# --------------------------------------------------------------------- timing
-def timed_iterations(fn: Callable[[], None], warmup: int, iterations: int) -> float:
-    """utils.py:14-29 without the device sync: mean wall-clock seconds per call."""
-    for _ in range(warmup):
-        fn()
-    start = time.perf_counter()
-    for _ in range(iterations):
-        fn()
-    return (time.perf_counter() - start) / max(iterations, 1)
 
 
 def to_numpy_bits(x: torch.Tensor) -> np.ndarray:

@@ -3,6 +3,7 @@
 // kernel families, event-timed loops and kernel metadata.
 #include "mb_common.hpp"
 
+#include <atomic>
 #include <cstring>
 #include <mutex>
 #include <string>
@@ -16,7 +17,37 @@ constexpr int kMaxDevices = 64;
 std::mutex g_props_mutex;
 DeviceProps g_props[kMaxDevices];
 bool g_props_valid[kMaxDevices] = {false};
+
+// Plan overrides, -1 = the library's own choice. Process-wide, lock-free reads.
+std::atomic<int64_t> g_tuning[MB_TUNE_COUNT] = {-1, -1, -1, -1, -1, -1, -1, -1, -1, -1};
+static_assert(MB_TUNE_COUNT == 10, "initialise every knob");
+
+struct KnobSpec {
+    const char* name;
+    bool (*valid)(int64_t);
+};
+
+bool is_bool(int64_t v) { return v == 0 || v == 1; }
+bool is_unroll(int64_t v) { return v == 1 || v == 2 || v == 4 || v == 8; }
+bool is_threads(int64_t v) { return v >= 64 && v <= 1024 && v % 64 == 0; }
+bool is_config(int64_t v) { return v >= 0 && v <= 3; }
+bool is_splits(int64_t v) { return v >= 1 && v <= 64; }
+bool is_mfma(int64_t v) { return v == 16 || v == 32; }
+
+const KnobSpec kKnobs[MB_TUNE_COUNT] = {
+    {"stream_unroll", is_unroll},   {"stream_nontemporal", is_bool}, {"stream_threads", is_threads},
+    {"stream_schedule", is_bool},   {"gemm_force_generic", is_bool}, {"gemm_no_small_m", is_bool},
+    {"gemm_tiled_config", is_config}, {"gemm_splits", is_splits},    {"gemm_fp8_mfma", is_mfma},
+    {"gemm_highp_staged", is_bool},
+};
+constexpr int kFirstGemmKnob = MB_TUNE_GEMM_FORCE_GENERIC;
+
 }  // namespace
+
+int64_t tuning(int knob) {
+    if (knob < 0 || knob >= MB_TUNE_COUNT) return -1;
+    return g_tuning[knob].load(std::memory_order_relaxed);
+}
 
 void set_error(const char* fmt, ...) {
     char buf[1024];
@@ -169,6 +200,23 @@ struct Json {
         key(k);
         s += v ? "true" : "false";
     }
+    // The knobs of [first, last) that hold an override, as a nested object.
+    void overrides(int first, int last) {
+        key("overrides");
+        s += "{";
+        bool any = false;
+        for (int i = first; i < last; ++i) {
+            const int64_t v = tuning(i);
+            if (v < 0) continue;
+            if (any) s += ",";
+            s += "\"";
+            s += kKnobs[i].name;
+            s += "\":";
+            s += std::to_string(v);
+            any = true;
+        }
+        s += "}";
+    }
     int emit(char* out, size_t cap) {
         s += "}";
         if (out == nullptr || cap < s.size() + 1) {
@@ -188,6 +236,23 @@ using namespace mb;
 extern "C" {
 
 int mb_abi_version(void) { return MB_ABI_VERSION; }
+
+int mb_set_tuning(int knob, int64_t value) {
+    clear_error();
+    if (knob < 0 || knob >= MB_TUNE_COUNT) {
+        set_error("unknown tuning knob %d", knob);
+        return MB_ERR_INVALID_ARG;
+    }
+    if (value != -1 && !kKnobs[knob].valid(value)) {
+        set_error("tuning knob %s cannot take %lld", kKnobs[knob].name, (long long)value);
+        return MB_ERR_INVALID_ARG;
+    }
+    g_tuning[knob].store(value, std::memory_order_relaxed);
+    return MB_OK;
+}
+
+int64_t mb_get_tuning(int knob) { return tuning(knob); }
+
 
 const char* mb_last_error(void) { return g_last_error.c_str(); }
 
@@ -281,6 +346,7 @@ int mb_kernel_info(int kind, int a, int b, int64_t m, int64_t n, int64_t k, char
         j.num("vector_bytes", 16);
         j.boolean("nontemporal", plan.nontemporal);
         j.str("arch", props->arch);
+        j.overrides(0, kFirstGemmKnob);
         return j.emit(json, cap);
     }
     if (kind == MB_KIND_GEMM) {
@@ -303,7 +369,9 @@ int mb_kernel_info(int kind, int a, int b, int64_t m, int64_t n, int64_t k, char
         j.num("split_k", plan.split_k);
         j.num("tile_group_m", plan.tile_group_m);
         j.num("workspace_bytes", (long long)plan.workspace);
+        j.str("fallback", plan.fallback);
         j.str("arch", props->arch);
+        j.overrides(kFirstGemmKnob, MB_TUNE_COUNT);
         return j.emit(json, cap);
     }
     set_error("unknown kernel info kind %d", kind);

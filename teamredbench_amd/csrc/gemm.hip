@@ -2,8 +2,6 @@
 // forwards the launch. Validation of dtype and sizes lives here.
 #include "gemm_common.hpp"
 
-#include <cstdlib>
-
 namespace mb {
 
 int gemm_plan(int dtype, int64_t M, int64_t N, int64_t K, const DeviceProps& props,
@@ -20,13 +18,15 @@ int gemm_plan(int dtype, int64_t M, int64_t N, int64_t K, const DeviceProps& pro
         return MB_ERR_INVALID_ARG;
     }
     if (dtype == MB_DT_FLOAT32 || dtype == MB_DT_FLOAT64) return gemm_highp_plan(dtype, M, N, K, props, plan);
-    if (std::getenv("MB_GEMM_FORCE_GENERIC") == nullptr && std::getenv("MB_GEMM_NO_GEMV") == nullptr &&
+    const bool generic_only = tuning(MB_TUNE_GEMM_FORCE_GENERIC) == 1;
+    if (!generic_only && tuning(MB_TUNE_GEMM_NO_SMALL_M) != 1 &&
         gemm_gemv_plan(dtype, M, N, K, props, plan) == MB_OK)
         return MB_OK;
-    if (std::getenv("MB_GEMM_FORCE_GENERIC") == nullptr &&
-        gemm_tiled_plan(dtype, M, N, K, props, plan) == MB_OK)
-        return MB_OK;
-    return gemm_generic_plan(dtype, M, N, K, plan);
+    const char* why = "forced by the gemm_force_generic override";
+    if (!generic_only && gemm_tiled_plan(dtype, M, N, K, props, plan, &why) == MB_OK) return MB_OK;
+    const int rc = gemm_generic_plan(dtype, M, N, K, plan);
+    plan->fallback = why;
+    return rc;
 }
 
 int gemm_launch(int dtype, const void* A, const void* B, void* C, int64_t M, int64_t N, int64_t K,

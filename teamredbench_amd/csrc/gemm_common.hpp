@@ -70,8 +70,9 @@ __device__ inline void store_out(void* C, int64_t idx, float v) {
 }
 
 int gemm_generic_plan(int dtype, int64_t M, int64_t N, int64_t K, GemmPlan* plan);
+// MB_ERR_SHAPE with *why naming the reason when no tiled configuration takes the shape.
 int gemm_tiled_plan(int dtype, int64_t M, int64_t N, int64_t K, const DeviceProps& props,
-                    GemmPlan* plan);
+                    GemmPlan* plan, const char** why);
 int gemm_tiled_launch(int dtype, const void* A, const void* B, void* C, int64_t M, int64_t N,
                       int64_t K, float alpha, void* workspace, const GemmPlan& plan, hipStream_t stream);
 int gemm_generic_launch(int dtype, const void* A, const void* B, void* C, int64_t M, int64_t N,

@@ -512,15 +512,27 @@ gemm_f64_dma_kernel(const double* __restrict__ A, const double* __restrict__ B, 
 // Which LDS-DMA ring a shape takes: 1 = the large tile (fp32 256 x 256, fp64
 // 256 x 128) when its tiles cover every CU, 2 = 128 x 128 when the shape
 // divides into it (2048^3 makes 64 large tiles but 256 small ones), 0 = the
-// register-staged kernel. K must be whole stages and the buffer offsets (B's
-// K x N bytes, a 256-row A panel) must stay within 31 bits.
-int highp_dma_config(bool f64, int64_t M, int64_t N, int64_t K, int cus) {
-    if (std::getenv("MB_GEMM_HIGHP_REGISTER") != nullptr) return 0;  // testing override: staged kernel
+// register-staged kernel, with *why naming the reason. K must be whole stages
+// and the buffer offsets (B's K x N bytes, a 256-row A panel) must stay
+// within 31 bits.
+int highp_dma_config(bool f64, int64_t M, int64_t N, int64_t K, int cus, const char** why) {
+    if (tuning(MB_TUNE_GEMM_HIGHP_STAGED) == 1) {
+        *why = "forced by the gemm_highp_staged override";
+        return 0;
+    }
     const int64_t e = f64 ? 8 : 4, stage_k = f64 ? kF64StageK : kF32StageK;
-    if (K % stage_k != 0 || K * N * e >= (int64_t(1) << 31) || 256 * K * e >= (int64_t(1) << 31)) return 0;
+    if (K % stage_k != 0) {
+        *why = f64 ? "K is not a multiple of 8" : "K is not a multiple of 16";
+        return 0;
+    }
+    if (K * N * e >= (int64_t(1) << 31) || 256 * K * e >= (int64_t(1) << 31)) {
+        *why = "operand offsets exceed 32-bit buffer addressing (K*N or 256*K bytes >= 2 GiB)";
+        return 0;
+    }
     const int64_t bm = 256, bn = f64 ? 128 : 256;
     if (M % bm == 0 && N % bn == 0 && (M / bm) * (N / bn) >= cus && (M / bm) * (N / bn) <= INT32_MAX) return 1;
     if (M % 128 == 0 && N % 128 == 0 && (M / 128) * (N / 128) <= INT32_MAX) return 2;
+    *why = "M or N is not a multiple of 128";
     return 0;
 }
 
@@ -566,7 +578,8 @@ int launch_typed(const void* A, const void* B, void* C, int64_t M, int64_t N, in
 
 int gemm_highp_plan(int dtype, int64_t M, int64_t N, int64_t K, const DeviceProps& props, GemmPlan* plan) {
     const bool f64 = dtype == MB_DT_FLOAT64;
-    const int cfg = highp_dma_config(f64, M, N, K, props.cu_count > 0 ? props.cu_count : 256);
+    const char* why = "";
+    const int cfg = highp_dma_config(f64, M, N, K, props.cu_count > 0 ? props.cu_count : 256, &why);
     if (cfg != 0) {
         int bm, bn;
         highp_dma_tile(f64, cfg, &bm, &bn);
@@ -609,6 +622,7 @@ int gemm_highp_plan(int dtype, int64_t M, int64_t N, int64_t K, const DeviceProp
     plan->split_k = 1;
     plan->tile_group_m = 1;
     plan->workspace = 0;
+    plan->fallback = why;
     plan->variant = kVariantHighp;
     return MB_OK;
 }

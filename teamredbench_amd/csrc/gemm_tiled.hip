@@ -967,7 +967,6 @@ constexpr TiledConfig kConfigs[] = {
     {128, 128, 2, 2, 3, 6, 4},  // 2: few tiles, N % 256 != 0: 64 x 64 per wave; 3 x 16 + 6 x 8 KiB
     {64, 128, 2, 2, 3, 6, 4},   // 3: small and skinny problems: 32 x 64 per wave; 3 x 8 + 6 x 8 KiB
 };
-constexpr int kNumConfigs = sizeof(kConfigs) / sizeof(kConfigs[0]);
 
 template <int DT, int CFG>
 int launch_cfg(const void* A, const void* B, void* C, int64_t M, int64_t N, int64_t K, float alpha,
@@ -1017,28 +1016,32 @@ int launch_dtype(const GemmPlan& plan, const void* A, const void* B, void* C, in
 
 }  // namespace
 
-// Picks the tiled configuration for a shape, or returns MB_ERR_SHAPE when the
-// shape does not divide into any of them (or its buffers need offsets beyond
-// the 32-bit range of buffer addressing).
+// Picks the tiled configuration for a shape, or returns MB_ERR_SHAPE with
+// *why set when the shape does not divide into any of them (or its buffers
+// need offsets beyond the 32-bit range of buffer addressing).
 int gemm_tiled_plan(int dtype, int64_t M, int64_t N, int64_t K, const DeviceProps& props,
-                    GemmPlan* plan) {
+                    GemmPlan* plan, const char** why) {
     const int64_t e = is_fp8(dtype) ? 1 : 2;
     const int64_t stage_k = kStageK / e;
     // N in 256-column tiles, or in 128-column tiles (configuration 2).
     const bool n128_only = N % 256 != 0;
-    if (K % stage_k != 0 || N % 128 != 0) return MB_ERR_SHAPE;
-    if (K * N * e >= (int64_t(1) << 31) || 256 * K * e >= (int64_t(1) << 31) || M >= (int64_t(1) << 31) ||
-        M * N >= (int64_t(1) << 31))
+    if (N % 128 != 0) {
+        *why = "N is not a multiple of 128";
         return MB_ERR_SHAPE;
+    }
+    if (K % stage_k != 0) {
+        *why = e == 1 ? "K is not a multiple of 64" : "K is not a multiple of 32";
+        return MB_ERR_SHAPE;
+    }
+    if (K * N * e >= (int64_t(1) << 31) || 256 * K * e >= (int64_t(1) << 31) || M >= (int64_t(1) << 31) ||
+        M * N >= (int64_t(1) << 31)) {
+        *why = "operand offsets exceed 32-bit buffer addressing (K*N or 256*K bytes, or M*N, >= 2^31)";
+        return MB_ERR_SHAPE;
+    }
     const int64_t cus = props.cu_count > 0 ? props.cu_count : 256;
     auto tiles = [&](int i) { return ((M + kConfigs[i].bm - 1) / kConfigs[i].bm) * (N / kConfigs[i].bn); };
-    int cfg = -1;
-    const char* force = std::getenv("MB_GEMM_TILED_CONFIG");  // tuning/testing override
-    if (force != nullptr && *force != '\0') {
-        const int f = std::atoi(force);
-        if (f >= 0 && f < kNumConfigs) cfg = f;
-    }
-    const bool env_forced = cfg >= 0;
+    int cfg = (int)tuning(MB_TUNE_GEMM_TILED_CONFIG);  // -1 unless forced
+    const bool config_forced = cfg >= 0;
     if (n128_only && cfg != 3) cfg = 2;
     const bool forced = cfg >= 0;
     if (cfg < 0) cfg = (tiles(0) >= cus && M % kConfigs[0].bm == 0) ? 0 : 1;
@@ -1116,22 +1119,21 @@ int gemm_tiled_plan(int dtype, int64_t M, int64_t N, int64_t K, const DeviceProp
     // (128 x 8192 x 8192 at 2 splits: bf16 2.5-9.5%, fp8 9%; fp16 ran 4-7%
     // slower at 128 x 8192 x 8192 and 128 x 4096 x 4096, so it keeps 128 x 128).
     const bool one_tile_rule = dtype != MB_DT_FLOAT16 && M <= kConfigs[2].bm && tiles(3) * splits <= cus;
-    if (!env_forced && cfg == 2 && (tiles(3) * splits * 2 <= cus || one_tile_rule)) cfg = 3;
-    const char* force_splits = std::getenv("MB_GEMM_SPLITS");  // tuning/testing override
-    if (force_splits != nullptr && *force_splits != '\0') {
-        const int f = std::atoi(force_splits);
-        if (f >= 1 && K % (stage_k * f) == 0) splits = f;
+    if (!config_forced && cfg == 2 && (tiles(3) * splits * 2 <= cus || one_tile_rule)) cfg = 3;
+    const int64_t force_splits = tuning(MB_TUNE_GEMM_SPLITS);
+    if (force_splits >= 1 && K % (stage_k * force_splits) == 0) splits = (int)force_splits;
+    if (tiles(cfg) * splits > INT32_MAX) {
+        *why = "more than 2^31 tiles";
+        return MB_ERR_SHAPE;
     }
-    if (tiles(cfg) * splits > INT32_MAX) return MB_ERR_SHAPE;
     const TiledConfig& c = kConfigs[cfg];
     // fp8 takes v_mfma_scale_f32_16x16x128_f8f6f4 on the 256 x 256 and
     // 128 x 256 tiles when every split holds an even number of stages (one
     // MFMA spans two): 2.3-4.2% faster than the 32x32x64 kernel on MI355X at
     // 4096^3-16384^3, equal at 8192 x 1024 x 8192. On 128 x 128 tiles (eight
     // MFMAs per step) it ran 2-4% slower, so those keep 32x32x64.
-    // MB_GEMM_FP8_MFMA=16 or 32 forces either (tuning/testing override).
-    const char* fp8_mfma = std::getenv("MB_GEMM_FP8_MFMA");
-    const int mfma_force = fp8_mfma != nullptr && *fp8_mfma != '\0' ? std::atoi(fp8_mfma) : 0;
+    // The gemm_fp8_mfma override (16 or 32) forces either.
+    const int64_t mfma_force = tuning(MB_TUNE_GEMM_FP8_MFMA);
     const bool mi16 = e == 1 && (K / splits) % (2 * stage_k) == 0 &&
                       (mfma_force == 16 || (mfma_force != 32 && c.bn == 256));
     const int frag = mi16 ? 16 : 32;

@@ -30,6 +30,11 @@ int hip_fail(hipError_t err, const char* what);
         }                                                \
     } while (0)
 
+// ---- plan overrides (mb_set_tuning) -----------------------------------------
+
+// The value a MB_TUNE_* knob holds: -1 for the library's own choice.
+int64_t tuning(int knob);
+
 // ---- device properties ----------------------------------------------------
 
 struct DeviceProps {
@@ -115,6 +120,7 @@ struct GemmPlan {
     int split_k = 1;
     int tile_group_m = 0;
     size_t workspace = 0;
+    const char* fallback = "";  // why a faster kernel family could not take the shape ("" if none)
     int variant = 0;            // kernel family selector, private to gemm*.hip
     int config = 0;             // configuration within the family
 };

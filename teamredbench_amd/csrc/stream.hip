@@ -346,9 +346,8 @@ ScalarKernel scalar_kernel_for(int op, int dtype) {
 
 // Tuned defaults per (op, dtype): blocks per CU, threads per block, 16-byte
 // chunks per thread per trip, nontemporal hint and schedule (0 grid-stride,
-// 1 contiguous span per block). Environment overrides exist for sweeps:
-// MB_STREAM_UNROLL (1,2,4,8), MB_STREAM_NT (0/1), MB_STREAM_THREADS (64..1024,
-// multiple of 64), MB_STREAM_SCHED (0/1).
+// 1 contiguous span per block). The MB_TUNE_STREAM_* knobs (mb_set_tuning)
+// override the last four for sweeps; their values are validated when set.
 struct StreamTuning {
     int blocks_per_cu;
     int threads;
@@ -367,10 +366,9 @@ StreamTuning default_tuning(int op, int dtype) {
     return {1, 256, 4, true, 0};
 }
 
-int env_int(const char* name, int fallback) {
-    const char* v = std::getenv(name);
-    if (v == nullptr || *v == '\0') return fallback;
-    return std::atoi(v);
+int knob_or(int knob, int fallback) {
+    const int64_t v = tuning(knob);
+    return v < 0 ? fallback : (int)v;
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
@@ -393,12 +391,10 @@ int stream_plan(int op, int dtype, const void* dst, const void* b, const void* c
         return MB_ERR_UNSUPPORTED;
     }
     StreamTuning t = default_tuning(op, dtype);
-    int u = env_int("MB_STREAM_UNROLL", t.unroll);
-    if (u != 1 && u != 2 && u != 4 && u != 8) u = t.unroll;
-    const bool nt = env_int("MB_STREAM_NT", t.nontemporal ? 1 : 0) != 0;
-    int threads = env_int("MB_STREAM_THREADS", t.threads);
-    if (threads < 64 || threads > 1024 || threads % 64 != 0) threads = t.threads;
-    const int sched = env_int("MB_STREAM_SCHED", t.schedule) == 1 ? 1 : 0;
+    const int u = knob_or(MB_TUNE_STREAM_UNROLL, t.unroll);
+    const bool nt = knob_or(MB_TUNE_STREAM_NONTEMPORAL, t.nontemporal ? 1 : 0) != 0;
+    const int threads = knob_or(MB_TUNE_STREAM_THREADS, t.threads);
+    const int sched = knob_or(MB_TUNE_STREAM_SCHEDULE, t.schedule);
     const int bpc = blocks_per_cu > 0 ? blocks_per_cu : t.blocks_per_cu;
 
     plan->threads = threads;

@@ -110,29 +110,7 @@ def build(verbose: bool = False, jobs: int | None = None) -> Path:
         raise BuildError("link failed:\n" + proc.stdout + proc.stderr)
     os.replace(tmp, out)
     (LIB_DIR / "BUILD_DIGEST").write_text(source_digest() + "\n", encoding="utf-8")
-    build_probes(hipcc)
     return out
-
-
-PROBE_SOURCES = {"mfma_ceiling": PACKAGE_DIR / "profiling" / "mfma_ceiling.hip"}
-
-
-def probe_path(name: str) -> Path:
-    return LIB_DIR / name
-
-
-def build_probes(hipcc: str | None = None) -> list[Path]:
-    """Compile the standalone measurement probes (executables, not part of the library) into LIB_DIR."""
-    hipcc = hipcc or find_hipcc()
-    built = []
-    for name, src in PROBE_SOURCES.items():
-        out = probe_path(name)
-        cmd = [hipcc, *[f for f in HIP_FLAGS if f != "-fPIC"], str(src), "-o", str(out)]
-        proc = subprocess.run(cmd, capture_output=True, text=True)
-        if proc.returncode != 0:
-            raise BuildError(f"{src.name} failed:\n" + proc.stdout + proc.stderr)
-        built.append(out)
-    return built
 
 
 if __name__ == "__main__":

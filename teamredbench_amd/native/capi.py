@@ -14,13 +14,14 @@ skipped record, the way the reference surfaces a failed hipcc build
 """
 from __future__ import annotations
 
+import contextlib
 import ctypes
 from dataclasses import dataclass
 import json
 import os
 from pathlib import Path
 import threading
-from typing import Any
+from typing import Any, Iterator
 
 from teamredbench_amd.native import build as _build
 
@@ -52,6 +53,20 @@ GEMM_OUTPUT_DTYPES = {"bfloat16": "bfloat16", "float16": "float16", "float8_e4m3
                       "float8_e5m2": "bfloat16", "float32": "float32", "float64": "float64"}
 
 KIND_STREAM, KIND_GEMM = 0, 1
+
+# Plan overrides (mb_set_tuning); names follow the "overrides" keys of mb_kernel_info.
+TUNING_KNOBS = {
+    "stream_unroll": 0,
+    "stream_nontemporal": 1,
+    "stream_threads": 2,
+    "stream_schedule": 3,
+    "gemm_force_generic": 4,
+    "gemm_no_small_m": 5,
+    "gemm_tiled_config": 6,
+    "gemm_splits": 7,
+    "gemm_fp8_mfma": 8,
+    "gemm_highp_staged": 9,
+}
 
 # Every symbol include/mi355bench.h declares, with (restype, argtypes).
 _u64, _i64, _vp, _cvp = ctypes.c_uint64, ctypes.c_int64, ctypes.c_void_p, ctypes.c_void_p
@@ -88,9 +103,11 @@ SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
         ctypes.c_int,
         [ctypes.c_int, ctypes.c_int, ctypes.c_int, _i64, _i64, _i64, ctypes.c_char_p, ctypes.c_size_t],
     ),
+    "mb_set_tuning": (ctypes.c_int, [ctypes.c_int, _i64]),
+    "mb_get_tuning": (_i64, [ctypes.c_int]),
 }
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 
 class NativeLibraryError(RuntimeError):
@@ -164,6 +181,28 @@ class NativeLibrary:
 
     def gemm_info(self, dtype: int, m: int, n: int, k: int) -> dict[str, Any]:
         return self.kernel_info(KIND_GEMM, dtype, 0, m, n, k)
+
+    # ---- plan overrides ----------------------------------------------------
+    def set_tuning(self, knob: str, value: int | None) -> None:
+        """Force a plan knob (see TUNING_KNOBS), or restore the library's choice with None."""
+        status = self.handle.mb_set_tuning(TUNING_KNOBS[knob], -1 if value is None else int(value))
+        self._check(status, f"mb_set_tuning({knob}={value})")
+
+    def get_tuning(self, knob: str) -> int | None:
+        value = int(self.handle.mb_get_tuning(TUNING_KNOBS[knob]))
+        return None if value < 0 else value
+
+    @contextlib.contextmanager
+    def tuned(self, **knobs: int | None) -> Iterator[None]:
+        """Hold the given knobs for the duration of a block, then restore what they held."""
+        saved = {name: self.get_tuning(name) for name in knobs}
+        try:
+            for name, value in knobs.items():
+                self.set_tuning(name, value)
+            yield
+        finally:
+            for name, value in saved.items():
+                self.set_tuning(name, value)
 
 
 _lock = threading.Lock()

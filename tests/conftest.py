@@ -39,3 +39,19 @@ def oracle_lib():
     from oracle import clib
 
     return clib.load()
+
+
+@pytest.fixture
+def tune(lib):
+    """Force plan knobs (mb_set_tuning) for one test: ``tune(gemm_splits=2)``. Every knob the test
+    touched is restored when it ends, so the overrides never leak into later tests."""
+    saved: dict[str, int | None] = {}
+
+    def set_knobs(**knobs: int | None) -> None:
+        for name, value in knobs.items():
+            saved.setdefault(name, lib.get_tuning(name))
+            lib.set_tuning(name, value)
+
+    yield set_knobs
+    for name, value in saved.items():
+        lib.set_tuning(name, value)

@@ -63,3 +63,24 @@ def test_abi_constants_match_the_header():
         assert int(consts["MB_DT_" + name.upper()]) == value
     assert int(consts["MB_ERR_SHAPE"]) == capi.MB_ERR_SHAPE
     assert int(consts["MB_ERR_WORKSPACE"]) == capi.MB_ERR_WORKSPACE
+    for name, value in capi.TUNING_KNOBS.items():
+        assert int(consts["MB_TUNE_" + name.upper()]) == value
+    assert int(consts["MB_TUNE_COUNT"]) == len(capi.TUNING_KNOBS)
+
+
+def test_tuning_knobs_validate_and_restore_without_a_gpu():
+    # mb_set_tuning / mb_get_tuning touch no device: they run here.
+    lib = capi.load_library()
+    assert all(lib.get_tuning(name) is None for name in capi.TUNING_KNOBS)
+    with lib.tuned(gemm_splits=4, stream_unroll=8):
+        assert lib.get_tuning("gemm_splits") == 4 and lib.get_tuning("stream_unroll") == 8
+    assert lib.get_tuning("gemm_splits") is None and lib.get_tuning("stream_unroll") is None
+    for name, bad in (("stream_unroll", 3), ("stream_threads", 96), ("stream_threads", 2048),
+                      ("gemm_tiled_config", 4), ("gemm_splits", 0), ("gemm_splits", 65), ("gemm_fp8_mfma", 8),
+                      ("gemm_force_generic", 2)):
+        with pytest.raises(capi.NativeLibraryError, match="cannot take") as err:
+            lib.set_tuning(name, bad)
+        assert err.value.status == capi.MB_ERR_INVALID_ARG
+        assert lib.get_tuning(name) is None          # a rejected value leaves the knob as it was
+    assert lib.handle.mb_set_tuning(capi.TUNING_KNOBS["gemm_splits"] + 100, 1) == capi.MB_ERR_INVALID_ARG
+    assert lib.handle.mb_get_tuning(-1) == -1

@@ -11,8 +11,6 @@ where the fp32 accumulation is exact.
 """
 from __future__ import annotations
 
-import os
-
 import numpy as np
 
 import pytest
@@ -39,8 +37,8 @@ UNIT = {"float32": 2.0**-24, "float64": 2.0**-53}
 def tiled_impl(dtype: str, k: int, info: dict) -> str:
     """The tiled kernel a plan takes: fp8 runs v_mfma_scale_f32_16x16x128_f8f6f4 on 256 x 256 and
     128 x 256 tiles when every split holds an even number of 64-byte stages, the 32x32 kernels
-    otherwise (MB_GEMM_FP8_MFMA=16 / 32 force either)."""
-    force = os.environ.get("MB_GEMM_FP8_MFMA", "")
+    otherwise (the gemm_fp8_mfma override, 16 or 32, forces either)."""
+    force = str(info["overrides"].get("gemm_fp8_mfma", ""))
     big_tile = info["tile_n"] == 256
     if dtype.startswith("float8") and (k // info["split_k"]) % 128 == 0 and \
             (force == "16" or (force != "32" and big_tile)):
@@ -85,10 +83,10 @@ def test_gemm_random_matches_fp32_matmul(lib, dtype, shape):
 @pytest.mark.parametrize("dtype", LOWP)
 @pytest.mark.parametrize("config", ["0", "1", "2", "3"])
 @pytest.mark.parametrize("shape", [(256, 256, 128), (256, 512, 64), (256, 512, 1024), (512, 256, 4096), (768, 1280, 384)])
-def test_tiled_configurations(lib, dtype, config, shape, monkeypatch):
+def test_tiled_configurations(lib, dtype, config, shape, tune):
     # Every tiled configuration on shapes it divides, selected through the
     # configuration override; the plan names the kernel that ran.
-    monkeypatch.setenv("MB_GEMM_TILED_CONFIG", config)
+    tune(gemm_tiled_config=int(config))
     m, n, k = shape
     info = lib.gemm_info(capi.DTYPES[dtype], m, n, k)
     assert info["implementation"] == tiled_impl(dtype, k, info)
@@ -100,12 +98,12 @@ def test_tiled_configurations(lib, dtype, config, shape, monkeypatch):
 @pytest.mark.parametrize("dtype", ["bfloat16", "float8_e4m3fn"])
 @pytest.mark.parametrize("config", ["0", "1", "2", "3"])
 @pytest.mark.parametrize("ksteps", [1, 2, 3, 4, 5, 6, 7, 8, 9, 11, 12, 13, 25, 37])
-def test_tiled_stage_counts(lib, dtype, config, ksteps, monkeypatch):
+def test_tiled_stage_counts(lib, dtype, config, ksteps, tune):
     # A is loaded two 64-byte K stages at a time: odd stage counts leave the
     # last pair half used, and counts around the 12-step unroll exercise the
     # tail loads that re-read the last stage / pair.
-    monkeypatch.setenv("MB_GEMM_TILED_CONFIG", config)
-    monkeypatch.setenv("MB_GEMM_SPLITS", "1")  # the 128-row tiles would split K for this few tiles
+    tune(gemm_tiled_config=int(config))
+    tune(gemm_splits=1)  # the 128-row tiles would split K for this few tiles
     k = ksteps * (64 if dtype.startswith("float8") else 32)
     m, n = 300, 512
     info = lib.gemm_info(capi.DTYPES[dtype], m, n, k)
@@ -116,9 +114,9 @@ def test_tiled_stage_counts(lib, dtype, config, ksteps, monkeypatch):
 
 @pytest.mark.parametrize("dtype", ["bfloat16", "float8_e4m3fn"])
 @pytest.mark.parametrize("splits, ksteps", [(3, 15), (3, 21), (5, 35), (7, 7)])
-def test_forced_splits_with_odd_stage_counts(lib, dtype, splits, ksteps, monkeypatch):
+def test_forced_splits_with_odd_stage_counts(lib, dtype, splits, ksteps, tune):
     # Each split runs ksteps / splits stages (odd here), writing fp32 partials.
-    monkeypatch.setenv("MB_GEMM_SPLITS", str(splits))
+    tune(gemm_splits=splits)
     k = ksteps * (64 if dtype.startswith("float8") else 32)
     m, n = 128, 512
     info = lib.gemm_info(capi.DTYPES[dtype], m, n, k)
@@ -129,10 +127,10 @@ def test_forced_splits_with_odd_stage_counts(lib, dtype, splits, ksteps, monkeyp
 
 @pytest.mark.parametrize("dtype", LOWP)
 @pytest.mark.parametrize("shape", [(512, 384, 256), (1000, 1152, 320), (64, 640, 512), (16, 1152, 4096), (3, 128, 64)])
-def test_n_multiple_of_128_takes_128x128_tiles(lib, dtype, shape, monkeypatch):
+def test_n_multiple_of_128_takes_128x128_tiles(lib, dtype, shape, tune):
     # Shapes with N a multiple of 128 but not 256 run the pipelined kernel on 128 x 128 tiles
     # (ragged M through the buffer range checks, skinny shapes with K splits).
-    monkeypatch.setenv("MB_GEMM_NO_GEMV", "1")  # keep M <= 4 on the tiled kernel too
+    tune(gemm_no_small_m=1)  # keep M <= 4 on the tiled kernel too
     m, n, k = shape
     info = lib.gemm_info(capi.DTYPES[dtype], m, n, k)
     assert info["implementation"] == tiled_impl(dtype, k, info) and info["tile_n"] == 128 and info["tile_m"] in (64, 128)
@@ -195,9 +193,9 @@ def test_skinny_shapes_split_k(lib, dtype, shape):
 @pytest.mark.parametrize("dtype", ["bfloat16", "float8_e4m3fn", "float8_e5m2"])
 @pytest.mark.parametrize("m", [1, 31, 127, 129, 300])
 @pytest.mark.parametrize("splits", ["1", "2", "3"])
-def test_ragged_m_and_forced_splits(lib, dtype, m, splits, monkeypatch):
-    monkeypatch.setenv("MB_GEMM_SPLITS", splits)
-    monkeypatch.setenv("MB_GEMM_NO_GEMV", "1")   # exercise the tiled kernel's splits at M = 1 too
+def test_ragged_m_and_forced_splits(lib, dtype, m, splits, tune):
+    tune(gemm_splits=int(splits))
+    tune(gemm_no_small_m=1)   # exercise the tiled kernel's splits at M = 1 too
     n, k = 512, 384
     info = lib.gemm_info(capi.DTYPES[dtype], m, n, k)
     assert info["split_k"] == int(splits)
@@ -363,7 +361,7 @@ def test_f32_lds_dma_kernel_selection(lib, shape, tile):
 
 
 @pytest.mark.parametrize("shape", [(4096, 4096, 64), (8192, 2048, 96), (1024, 1536, 48), (2048, 2048, 16)])
-def test_f32_lds_dma_against_float64_brute_force(lib, shape, monkeypatch):
+def test_f32_lds_dma_against_float64_brute_force(lib, shape, tune):
     # The LDS-DMA kernel sums each stage's 16 K values in a permuted order (lane half h takes K 8h + t
     # at step t); every element must still sit within the fp32 accumulation bound of an fp64
     # brute force, and the staged kernel (forced) must agree with it to the same bound.
@@ -377,7 +375,7 @@ def test_f32_lds_dma_against_float64_brute_force(lib, shape, monkeypatch):
     mag = torch.from_numpy(np.abs(a64)) @ torch.from_numpy(np.abs(b64))
     bound = ref.abs() * UNIT["float32"] + (k + 1) * UNIT["float32"] * mag
     assert torch.all((got - ref).abs() <= bound)
-    monkeypatch.setenv("MB_GEMM_HIGHP_REGISTER", "1")
+    tune(gemm_highp_staged=1)
     assert lib.gemm_info(capi.DT_FLOAT32, m, n, k)["implementation"] == "gfx950_mfma_f32_32x32x2"
     staged = _gemm(lib, "float32", ops["a"], ops["b"]).double()
     assert torch.all((staged - ref).abs() <= bound)
@@ -397,7 +395,7 @@ def test_f64_lds_dma_kernel_selection(lib, shape, tile):
 
 
 @pytest.mark.parametrize("shape", [(4096, 8192, 40), (8192, 4096, 24), (1024, 1536, 40), (2048, 2048, 8)])
-def test_f64_lds_dma_against_float64_brute_force(lib, shape, monkeypatch):
+def test_f64_lds_dma_against_float64_brute_force(lib, shape, tune):
     # K permuted inside each stage (lane group g takes K 2g + t at step t); every element within the
     # fp64 accumulation bound of the brute force, and the staged kernel (forced) within the same bound.
     m, n, k = shape
@@ -410,7 +408,7 @@ def test_f64_lds_dma_against_float64_brute_force(lib, shape, monkeypatch):
     mag = torch.from_numpy(np.abs(a64)) @ torch.from_numpy(np.abs(b64))
     bound = ref.abs() * UNIT["float64"] + (k + 1) * UNIT["float64"] * mag
     assert torch.all((got - ref).abs() <= bound)
-    monkeypatch.setenv("MB_GEMM_HIGHP_REGISTER", "1")
+    tune(gemm_highp_staged=1)
     assert lib.gemm_info(capi.DT_FLOAT64, m, n, k)["implementation"] == "gfx950_mfma_f64_16x16x4"
     staged = _gemm(lib, "float64", ops["a"], ops["b"])
     assert torch.all((staged - ref).abs() <= bound)
@@ -472,12 +470,12 @@ def test_small_m_one_split_writes_c_directly(lib):
 
 @pytest.mark.parametrize("dtype", ["bfloat16", "float8_e4m3fn"])
 @pytest.mark.parametrize("config, splits", [("1", 4), ("2", 2), ("2", 8)])
-def test_split_k_reduction_ignores_workspace_contents(lib, dtype, config, splits, monkeypatch):
+def test_split_k_reduction_ignores_workspace_contents(lib, dtype, config, splits, tune):
     # The caller's workspace is never cleared: every split writes its whole fp32 partial before the
     # reduction reads it, so whatever the workspace held (0xFF bytes, random bytes, zeros, the same
     # call's partials, another shape's partials), the split-K result must be the same, bit for bit.
-    monkeypatch.setenv("MB_GEMM_TILED_CONFIG", config)
-    monkeypatch.setenv("MB_GEMM_SPLITS", str(splits))
+    tune(gemm_tiled_config=int(config))
+    tune(gemm_splits=splits)
     m, n, k = 100, 1024, 64 * 8 * splits
     dt = capi.DTYPES[dtype]
     info = lib.gemm_info(dt, m, n, k)
@@ -518,18 +516,18 @@ def test_split_k_reduction_ignores_workspace_contents(lib, dtype, config, splits
 @pytest.mark.parametrize("dtype", ["float8_e4m3fn", "float8_e5m2"])
 @pytest.mark.parametrize("config, shape", [("0", (512, 512, 1024)), ("1", (384, 768, 640)), ("2", (200, 384, 1152)),
                                            ("0", (256, 256, 128)), ("3", (136, 384, 1024))])
-def test_fp8_16x16_and_32x32_kernels_agree(lib, dtype, config, shape, monkeypatch):
-    # The 16x16x128 kernel and the 32x32x64 one (MB_GEMM_FP8_MFMA=32) on the same inputs: both within
+def test_fp8_16x16_and_32x32_kernels_agree(lib, dtype, config, shape, tune):
+    # The 16x16x128 kernel and the 32x32x64 one (gemm_fp8_mfma = 32) on the same inputs: both within
     # the fp8 tolerance of the fp32 reference, and within fp32 summation-order noise of each other.
-    monkeypatch.setenv("MB_GEMM_TILED_CONFIG", config)
-    monkeypatch.setenv("MB_GEMM_SPLITS", "1")
+    tune(gemm_tiled_config=int(config))
+    tune(gemm_splits=1)
     m, n, k = shape
     dt = capi.DTYPES[dtype]
     ops = rp.gemm_inputs(m, n, k, dtype, seed=k)
     a, b = ops["a"].cuda(), ops["b"].cuda()
     out = {}
     for mfma in ("16", "32"):
-        monkeypatch.setenv("MB_GEMM_FP8_MFMA", mfma)
+        tune(gemm_fp8_mfma=int(mfma))
         info = lib.gemm_info(dt, m, n, k)
         assert info["implementation"] == f"gfx950_mfma{mfma}_lds_dma" and info["frag_m"] == int(mfma)
         c = torch.full((m, n), float("nan"), dtype=rp.gemm_output_dtype(dtype), device="cuda")
@@ -556,3 +554,32 @@ def test_mostly_empty_last_round_takes_128_row_tiles(lib, dtype, shape, tile_m):
     m, n, k = shape
     info = lib.gemm_info(capi.DTYPES[dtype], m, n, k)
     assert (info["tile_m"], info["tile_n"], info["split_k"]) == (tile_m, 256, 1)
+
+
+def test_overrides_are_reported_and_the_environment_is_ignored(lib, tune, monkeypatch):
+    # Plans change only through mb_set_tuning, and kernel_info names every override in force.
+    shape = (128, 512, 3 * 64 * 8)
+    base = lib.gemm_info(capi.DT_BFLOAT16, *shape)
+    assert base["overrides"] == {}
+    monkeypatch.setenv("MB_GEMM_SPLITS", "3")   # the variable an earlier library read: no effect now
+    assert lib.gemm_info(capi.DT_BFLOAT16, *shape) == base
+    tune(gemm_splits=3)
+    forced = lib.gemm_info(capi.DT_BFLOAT16, *shape)
+    assert forced["split_k"] == 3 and forced["overrides"] == {"gemm_splits": 3}
+    assert lib.stream_info(capi.OP_TRIAD, capi.DT_FLOAT32, 1 << 20)["overrides"] == {}
+    with pytest.raises(capi.NativeLibraryError) as err:
+        lib.set_tuning("gemm_tiled_config", 4)
+    assert err.value.status == capi.MB_ERR_INVALID_ARG
+
+
+@pytest.mark.parametrize("dtype, shape, impl, reason", [
+    ("bfloat16", (256, 200, 256), "gfx950_mfma_generic", "N is not a multiple of 128"),
+    ("float8_e4m3fn", (256, 256, 96), "gfx950_mfma_generic", "K is not a multiple of 64"),
+    ("float32", (300, 200, 64), "gfx950_mfma_f32_32x32x2", "M or N is not a multiple of 128"),
+    ("bfloat16", (256, 256, 256), "gfx950_mfma32_lds_dma", ""),
+])
+def test_kernel_info_names_the_fallback(lib, dtype, shape, impl, reason):
+    # A shape the pipelined kernels cannot take runs on a bounds-checked kernel, and the plan says why.
+    info = lib.gemm_info(capi.DTYPES[dtype], *shape)
+    assert info["implementation"].startswith(impl) and info["fallback"] == reason
+    _check_random(lib, dtype, *shape, seed=1)

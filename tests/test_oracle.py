@@ -247,6 +247,24 @@ def test_rel_frobenius_known_value():
     assert rp.rel_frobenius(torch.tensor([3.0, 4.5]), ref) == pytest.approx(0.1)
 
 
+def test_max_abs_over_max_ref_known_values():
+    # The reference harness's criterion (tests/native/gemm_parity.hip.cpp:160-178): the largest
+    # absolute difference over the largest |reference| entry. Chosen so that the plausible slips give
+    # other numbers: max(ref) instead of max|ref| gives 0.25 / 1, max|out| instead of max|ref| gives
+    # 0.25 / 3.75, the mean difference instead of the max gives 0.25 / 4 / 4, a signed max gives 0.
+    ref = torch.tensor([[1.0, -4.0], [2.0, 0.5]])
+    out = torch.tensor([[1.0, -3.75], [2.0, 0.5]])
+    assert rp.max_abs_over_max_ref(out, ref) == 0.0625
+    assert rp.max_abs_over_max_ref(ref, ref) == 0.0
+    # half-precision inputs are compared as their exact values (no rounding of the difference):
+    # 1 + 2^-7 and 1 are both bf16 values; the difference 2^-7 over max|ref| = 2 is 2^-8 exactly
+    r16 = torch.tensor([1.0, 2.0], dtype=torch.bfloat16)
+    o16 = torch.tensor([1.0 + 2.0**-7, 2.0], dtype=torch.bfloat16)
+    assert rp.max_abs_over_max_ref(o16, r16) == 2.0**-8
+    # an all-zero reference divides by the harness's 1e-12 floor
+    assert rp.max_abs_over_max_ref(torch.tensor([1e-13]), torch.tensor([0.0])) == pytest.approx(0.1)
+
+
 # ---------------------------------------------------------------- GEMM
 def test_gemm_reference_matches_float64_brute_force():
     for m, n, k in [(1, 1, 1), (7, 5, 3), (33, 17, 65), (64, 48, 96)]:

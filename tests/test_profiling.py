@@ -211,27 +211,3 @@ def test_suite_summary_formats_gemm_records(tmp_path: Path):
     assert len(gemm) == 3
     assert gemm[1].split() == ["gemm_16x8192x8192", "bfloat16", "128x256", "4", "26.25", "81.8", "3.3", "5133"]
     assert gemm[2].split() == ["gemm_2048x2048x2048", "bfloat16", "128x128", "1", "21.30", "806.5", "32.3", "-"]
-
-
-def test_mfma_ceiling_probe_output_parses_and_formats():
-    from teamredbench_amd.profiling import mfma_ceiling
-
-    out = "\n".join([
-        "warm-up text",
-        '{"instruction": "v_mfma_f32_32x32x16_bf16", "dtype": "bfloat16", "sustained_tflops": 1699.8, '
-        '"peak_tflops": 2500.0, "fraction_of_peak": 0.6799, "ms_per_launch": 6.3}',
-        '{"not": "a probe row"}',
-    ])
-    rows = mfma_ceiling.parse(out)
-    assert len(rows) == 1 and rows[0]["dtype"] == "bfloat16"
-    table = mfma_ceiling.format_table(rows)
-    assert "v_mfma_f32_32x32x16_bf16" in table and "68.0%" in table
-
-
-def test_mfma_ceiling_probe_is_built_with_the_library():
-    from teamredbench_amd.native import build
-
-    if not build.library_path().exists():
-        pytest.skip("library not built")
-    exe = build.probe_path("mfma_ceiling")
-    assert exe.exists() and os.access(exe, os.X_OK)
