@@ -12,7 +12,8 @@
  * Conventions (all entry points):
  *   - Plain pointers and sizes only. Device buffers are owned by the caller;
  *     the library never allocates or frees device memory except the hipEvents
- *     used by the mb_time_* entry points.
+ *     used by the mb_time_* entry points and the fixed per-GPU scratch array
+ *     that mb_gemm_noalloc uses (a static device variable of the library).
  *   - `stream` is a hipStream_t passed as void* (NULL = the null stream).
  *     Work is enqueued asynchronously; nothing synchronises except mb_time_*.
  *   - Return 0 on success, a negative MB_ERR_* for a rejected argument, or a
@@ -30,7 +31,7 @@
 extern "C" {
 #endif
 
-#define MB_ABI_VERSION 2
+#define MB_ABI_VERSION 3
 
 /* Status codes (negative = rejected by the library before any launch). */
 #define MB_OK 0
@@ -122,6 +123,26 @@ int mb_gemm(int dtype, const void* A, const void* B, void* C, int64_t M,
 /* Workspace bytes mb_gemm needs for this dtype and shape (0 if none). */
 size_t mb_gemm_workspace_size(int dtype, int64_t M, int64_t N, int64_t K);
 
+/*
+ * mb_gemm_noalloc -- mb_gemm without a workspace argument, for callers that
+ * cannot allocate device memory (code under HIP graph capture, serving loops,
+ * harnesses that forbid hipMalloc). It has no counterpart in the reference.
+ *
+ * Same arguments, kernels and results as mb_gemm. The split-K / small-M
+ * partial sums go to a library-owned device array of
+ * MB_NOALLOC_SCRATCH_BYTES per GPU, which each GPU holds until the process
+ * ends; the call itself allocates nothing. Shapes whose plan needs more
+ * scratch than that return MB_ERR_WORKSPACE before any launch. The first
+ * call on a device resolves that device's array address (not an
+ * allocation); make it before a capture if the capture must not see it.
+ * Every call on one GPU shares that GPU's array, and every call writes all
+ * the partials it reads, so nothing carries over between calls; calls that
+ * overlap on one GPU (concurrent streams or threads) race on the array.
+ */
+#define MB_NOALLOC_SCRATCH_BYTES (64u << 20)
+int mb_gemm_noalloc(int dtype, const void* A, const void* B, void* C,
+                    int64_t M, int64_t N, int64_t K, float scale_a,
+                    float scale_b, void* stream);
 
 /*
  * mb_time_gemm -- warmup + event-timed loop of mb_gemm launches.

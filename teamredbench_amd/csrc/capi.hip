@@ -228,6 +228,33 @@ struct Json {
     }
 };
 
+// Scratch for mb_gemm_noalloc: the split-K and small-M partial planes
+// (split_k x M x N fp32) that mb_gemm takes from a caller's workspace. One
+// copy per device, held for the life of the process. Host code never uses
+// the symbol's name as an address: it resolves each device's copy with
+// hipGetSymbolAddress once (scratch_address) and passes that pointer.
+static __device__ __align__(256) unsigned char scratch[MB_NOALLOC_SCRATCH_BYTES];
+
+std::mutex g_scratch_mutex;
+void* g_scratch_ptr[kMaxDevices] = {nullptr};
+
+// This device's copy of `scratch`, resolved on the first call per device
+// (with that device current) and cached.
+int scratch_address(int device, void** out) {
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if (g_scratch_ptr[device] == nullptr) {
+        void* ptr = nullptr;
+        MB_HIP_TRY(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)));
+        if (ptr == nullptr) {
+            set_error("hipGetSymbolAddress(scratch) returned NULL on device %d", device);
+            return MB_ERR_DEVICE;
+        }
+        g_scratch_ptr[device] = ptr;
+    }
+    *out = g_scratch_ptr[device];
+    return MB_OK;
+}
+
 }  // namespace
 }  // namespace mb
 
@@ -302,6 +329,27 @@ int mb_gemm(int dtype, const void* A, const void* B, void* C, int64_t M, int64_t
         return rc;
     return gemm_launch(dtype, A, B, C, M, N, K, scale_a, scale_b, workspace, plan,
                        static_cast<hipStream_t>(stream));
+}
+
+int mb_gemm_noalloc(int dtype, const void* A, const void* B, void* C, int64_t M, int64_t N, int64_t K,
+                    float scale_a, float scale_b, void* stream) {
+    clear_error();
+    const DeviceProps* props = nullptr;
+    int rc = device_for_launch(&props);
+    if (rc != MB_OK) return rc;
+    GemmPlan plan;
+    if ((rc = gemm_plan(dtype, M, N, K, *props, &plan)) != MB_OK) return rc;
+    if (plan.workspace > (size_t)MB_NOALLOC_SCRATCH_BYTES) {
+        set_error("GEMM %s %lldx%lldx%lld needs %zu scratch bytes; mb_gemm_noalloc holds %zu "
+                  "(use mb_gemm with a caller workspace)",
+                  dtype_name(dtype), (long long)M, (long long)N, (long long)K, plan.workspace,
+                  (size_t)MB_NOALLOC_SCRATCH_BYTES);
+        return MB_ERR_WORKSPACE;
+    }
+    void* ws = nullptr;
+    if (plan.workspace > 0 && (rc = scratch_address(props->device, &ws)) != MB_OK) return rc;
+    if ((rc = check_gemm_args(dtype, A, B, C, M, N, K, ws, plan.workspace, plan)) != MB_OK) return rc;
+    return gemm_launch(dtype, A, B, C, M, N, K, scale_a, scale_b, ws, plan, static_cast<hipStream_t>(stream));
 }
 
 int mb_time_gemm(int dtype, const void* A, const void* B, void* C, int64_t M, int64_t N, int64_t K,

@@ -32,6 +32,8 @@ MB_ERR_SHAPE = -3
 MB_ERR_WORKSPACE = -4
 MB_ERR_DEVICE = -5
 
+NOALLOC_SCRATCH_BYTES = 64 << 20   # MB_NOALLOC_SCRATCH_BYTES
+
 OP_COPY, OP_SCALE, OP_TRIAD = 0, 1, 2
 OPS = {"copy": OP_COPY, "scale": OP_SCALE, "triad": OP_TRIAD}
 
@@ -92,6 +94,10 @@ SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
         ],
     ),
     "mb_gemm_workspace_size": (ctypes.c_size_t, [ctypes.c_int, _i64, _i64, _i64]),
+    "mb_gemm_noalloc": (
+        ctypes.c_int,
+        [ctypes.c_int, _cvp, _cvp, _vp, _i64, _i64, _i64, ctypes.c_float, ctypes.c_float, _vp],
+    ),
     "mb_time_gemm": (
         ctypes.c_int,
         [
@@ -107,7 +113,7 @@ SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
     "mb_get_tuning": (_i64, [ctypes.c_int]),
 }
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 
 class NativeLibraryError(RuntimeError):
@@ -157,6 +163,13 @@ class NativeLibrary:
             stream or None,
         )
         self._check(status, "mb_gemm")
+
+    def gemm_noalloc(self, dtype: int, a: int, b: int, c: int, m: int, n: int, k: int, scale_a: float = 1.0,
+                     scale_b: float = 1.0, stream: int | None = None) -> None:
+        """mb_gemm with the library's own per-GPU scratch array instead of a workspace argument."""
+        status = self.handle.mb_gemm_noalloc(dtype, a, b, c, m, n, k, float(scale_a), float(scale_b),
+                                             stream or None)
+        self._check(status, "mb_gemm_noalloc")
 
     def time_gemm(self, dtype: int, a: int, b: int, c: int, m: int, n: int, k: int, scale_a: float,
                   scale_b: float, workspace: int | None, workspace_bytes: int, warmup: int, iterations: int,

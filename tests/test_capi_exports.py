@@ -66,6 +66,8 @@ def test_abi_constants_match_the_header():
     for name, value in capi.TUNING_KNOBS.items():
         assert int(consts["MB_TUNE_" + name.upper()]) == value
     assert int(consts["MB_TUNE_COUNT"]) == len(capi.TUNING_KNOBS)
+    shift = re.search(r"#define MB_NOALLOC_SCRATCH_BYTES \((\d+)u << (\d+)\)", text)
+    assert shift and int(shift.group(1)) << int(shift.group(2)) == capi.NOALLOC_SCRATCH_BYTES
 
 
 def test_tuning_knobs_validate_and_restore_without_a_gpu():
