@@ -156,6 +156,23 @@ int mb_time_gemm(int dtype, const void* A, const void* B, void* C, int64_t M,
                  int iterations, void* stream, double* elapsed_s);
 
 /*
+ * mb_time_gemm_rotating -- mb_time_gemm over `sets` operand sets: launch i
+ * (warmup launches included) multiplies A[i % sets] by B[i % sets] into
+ * C[i % sets], all of one shape, sharing `workspace` (the launches run in
+ * order on `stream`). With sets whose operands together exceed the 256 MB
+ * Infinity Cache, every launch reads its operands from HBM, so the time is
+ * that of the HBM-bound case rather than of operands left in the cache by
+ * the previous launch. No counterpart in the reference, whose executable
+ * times one operand set (mfu_gemm_lowp.hip.hpp:447-485).
+ */
+int mb_time_gemm_rotating(int dtype, const void* const* A,
+                          const void* const* B, void* const* C, int sets,
+                          int64_t M, int64_t N, int64_t K, float scale_a,
+                          float scale_b, void* workspace,
+                          size_t workspace_bytes, int warmup, int iterations,
+                          void* stream, double* elapsed_s);
+
+/*
  * mb_kernel_info -- JSON object describing the kernel configuration the
  * library picks for a case, written NUL-terminated into json[0..cap).
  *

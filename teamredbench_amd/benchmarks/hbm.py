@@ -47,15 +47,32 @@ class HbmBandwidthBenchmark(Benchmark):
     default_metrics = ["hbm_bandwidth_gbps", "hbm_efficiency_pct", "latency_us"]
 
     # ------------------------------------------------------------ shared
-    def _run_mode(self, mode: str, src: Any, dst: Any, aux: Any, scale: float) -> None:
-        if mode == "copy":
-            dst.copy_(src)
-        elif mode == "scale":
-            self.torch.mul(src, scale, out=dst)
-        elif mode == "triad":
-            self.torch.add(src, aux, alpha=scale, out=dst)
+    # The reference's stream ops (hbm.py:29-39) as PyTorch computes them: the
+    # torch backend times these, and the native backend checks its output
+    # against them on the same arrays.
+    TORCH_OPS = {
+        "copy": lambda torch, dst, src, aux, s: dst.copy_(src),
+        "scale": lambda torch, dst, src, aux, s: torch.mul(src, s, out=dst),
+        "triad": lambda torch, dst, src, aux, s: torch.add(src, aux, alpha=s, out=dst),
+    }
+
+    def _device_problem(self) -> str | None:
+        """Why no GPU case can run here, or None."""
+        if self.context.torch_module is None:
+            return "PyTorch is not installed."
+        if not rocm_device_available(self.context.torch_module):
+            return "No ROCm device visible to PyTorch."
+        return None
+
+    def _inputs(self, spec, mode: str, numel: int, seed: int):
+        """(src, aux or None): uniform[-1, 1] from `seed` / `seed + 1` for the float types and int8
+        (drawn on the device), torch's generic random fill for any other type."""
+        torch = self.torch
+        if spec.kind == "float" or spec.name == "int8":
+            make = lambda s: seeded_uniform(torch, numel, spec.name, self.device, s)  # noqa: E731
         else:
-            raise KeyError(f"Unknown HBM mode: {mode}")
+            make = lambda s: make_tensor(torch, spec, (numel,), self.device)  # noqa: E731
+        return make(seed), (make(seed + 1) if mode == "triad" else None)
 
     def _common_params(self) -> tuple[int, int, int, list[str], float]:
         size_mib = int(self.params.get("size_mib", 1024))
@@ -136,9 +153,10 @@ class HbmBandwidthBenchmark(Benchmark):
             lib = capi.load_library()
         except capi.NativeLibraryError as exc:
             return skip_all(str(exc))
-        torch = self.context.torch_module
-        if not rocm_device_available(torch):
-            return skip_all("No ROCm device visible to PyTorch.")
+        problem = self._device_problem()
+        if problem is not None:
+            return skip_all(problem)
+        torch = self.torch
         self.set_device()
 
         records: list[BenchmarkRecord] = []
@@ -163,8 +181,7 @@ class HbmBandwidthBenchmark(Benchmark):
     def _capi_case(self, lib, torch, spec, mode, numel, case, meta, scale, bpc, warmup, iterations, seed, verify,
                    peak) -> BenchmarkRecord:
         device = self.device
-        src = seeded_uniform(torch, numel, spec.name, device, seed)
-        aux = seeded_uniform(torch, numel, spec.name, device, seed + 1) if mode == "triad" else None
+        src, aux = self._inputs(spec, mode, numel, seed)
         dst = torch.empty_like(src)
         op, dt = capi.OPS[mode], capi.DTYPES[spec.name]
         stream = torch.cuda.current_stream(device).cuda_stream
@@ -177,59 +194,54 @@ class HbmBandwidthBenchmark(Benchmark):
         meta["cache_resident"] = working_set <= INFINITY_CACHE_BYTES
         if verify:
             ref = torch.empty_like(src)
-            self._run_mode(mode, src, ref, aux, scale)
+            self.TORCH_OPS[mode](torch, ref, src, aux, scale)
             meta["parity"] = stream_parity(torch, mode, dst, ref)
             del ref
-        return self.emit_record(
-            BenchmarkRecord(
-                benchmark=self.name,
-                case=case,
-                dtype=spec.name,
-                raw_metrics={"elapsed_s": elapsed, "moved_bytes": moved, "peak_bandwidth_gbps": peak},
-                metadata=meta,
-            )
-        )
+        return self.measured(case=case, dtype=spec.name, metadata=meta,
+                             raw_metrics={"elapsed_s": elapsed, "moved_bytes": moved, "peak_bandwidth_gbps": peak})
 
     # ------------------------------------------------------------- torch
+    # The reference torch path (hbm.py:174-240): the op through PyTorch's own
+    # kernels, timed by wall clock between device synchronisations
+    # (utils.timed_iterations), the reference's timing for this backend. It
+    # runs on the native path's seeded inputs (the reference draws unseeded
+    # randn), so the two backends' records time the same data; cases and
+    # sizes follow the same params (size_mib or elements).
     def _run_torch(self) -> list[BenchmarkRecord]:
-        if self.context.torch_module is None:
-            return [self.skip(case="global", dtype="n/a", error="PyTorch is not installed.")]
-        torch = self.torch
-        if not rocm_device_available(torch):
-            return [self.skip(case="global", dtype="n/a", error="No ROCm device visible to PyTorch.")]
+        problem = self._device_problem()
+        if problem is not None:
+            return [self.skip(case="global", dtype="n/a", error=problem)]
         self.set_device()
-        size_mib, warmup, iterations, modes, scale = self._common_params()
-        records: list[BenchmarkRecord] = []
-        for spec in self.selected_dtype_specs():
-            numel = max(size_mib * 1024 * 1024 // spec.bytes_per_element, 1)
-            for mode in modes:
-                case = f"{mode}_{size_mib}MiB"
-                try:
-                    src = make_tensor(torch, spec, (numel,), self.device)
-                    dst = torch.empty_like(src)
-                    aux = make_tensor(torch, spec, (numel,), self.device) if mode == "triad" else None
-                    elapsed = timed_iterations(lambda: self._run_mode(mode, src, dst, aux, scale), torch_module=torch,
-                                               warmup=warmup, iterations=iterations)
-                except Exception as exc:  # noqa: BLE001 -- any failure skips this case only
-                    records.append(self.skip(case=case, dtype=spec.name, error=str(exc),
-                                             metadata={"backend": "torch", "mode": mode, "size_mib": size_mib}))
-                    continue
-                records.append(
-                    self.emit_record(
-                        BenchmarkRecord(
-                            benchmark=self.name,
-                            case=case,
-                            dtype=spec.name,
-                            raw_metrics={
-                                "elapsed_s": elapsed,
-                                "moved_bytes": MODE_BYTE_FACTORS[mode] * numel * spec.bytes_per_element,
-                                "peak_bandwidth_gbps": self.context.hardware_profile.peak_hbm_bandwidth_gbps,
-                            },
-                            metadata={"backend": "torch", "mode": mode, "size_mib": size_mib, "elements": numel},
-                        )
-                    )
-                )
-        return records
+        _, warmup, iterations, modes, scale = self._common_params()
+        seed = int(self.params.get("seed", 0))
+        peak = self.context.hardware_profile.peak_hbm_bandwidth_gbps
+        return [self._torch_case(spec, mode, numel, suffix, size_meta, scale, warmup, iterations, seed, peak)
+                for spec in self.selected_dtype_specs()
+                for numel, suffix, size_meta in self._sizes(spec)
+                for mode in modes]
+
+    def _torch_case(self, spec, mode, numel, suffix, size_meta, scale, warmup, iterations, seed,
+                    peak) -> BenchmarkRecord:
+        torch = self.torch
+        case, meta = f"{mode}_{suffix}", {"backend": "torch", "mode": mode, **size_meta}
+        if mode not in self.TORCH_OPS:
+            return self.skip(case=case, dtype=spec.name, error=f"Unknown HBM mode: {mode}", metadata=meta)
+        op = self.TORCH_OPS[mode]
+        try:
+            src, aux = self._inputs(spec, mode, numel, seed)
+            dst = torch.empty_like(src)
+            elapsed = timed_iterations(lambda: op(torch, dst, src, aux, scale), torch_module=torch, warmup=warmup,
+                                       iterations=iterations)
+        except Exception as exc:  # noqa: BLE001 -- an op torch cannot run for this dtype skips this case only
+            return self.skip(case=case, dtype=spec.name, error=str(exc), metadata=meta)
+        finally:
+            torch.cuda.empty_cache()
+        working_set = (3 if mode == "triad" else 2) * numel * spec.bytes_per_element
+        meta.update(working_set_bytes=working_set, cache_resident=working_set <= INFINITY_CACHE_BYTES,
+                    timing="wall_clock")
+        moved = MODE_BYTE_FACTORS[mode] * numel * spec.bytes_per_element
+        return self.measured(case=case, dtype=spec.name, metadata=meta,
+                             raw_metrics={"elapsed_s": elapsed, "moved_bytes": moved, "peak_bandwidth_gbps": peak})
 
     def run(self) -> list[BenchmarkRecord]:
         backend = str(self.params.get("backend", "torch")).lower()

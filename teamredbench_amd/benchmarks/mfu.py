@@ -7,7 +7,13 @@ API and record shape follow src/teamredbench/benchmarks/mfu.py:
           default true; at most `verify_max_rows` rows of C, default 4096),
           warmup_seconds (default 0: untimed warmup lasts at least this
           long, more launches than `warmup` if need be -- the part leaves
-          its low-power clock state only after tens of ms of MFMA work)
+          its low-power clock state only after tens of ms of MFMA work),
+          operand_sets ("auto", or a count: the native timed loop cycles
+          through that many copies of A, B and C; "auto" takes enough
+          copies to exceed three times the 256 MB Infinity Cache for a
+          memory-bound shape -- arithmetic intensity below the dtype's
+          ridge point, peak_tops / peak HBM bandwidth -- whose operands would
+          otherwise stay cache-resident between launches, and 1 otherwise)
   record: case "gemm_<m>x<n>x<k>"; raw_metrics elapsed_s / achieved_ops
           (= matmul_ops_factor * m * n * k) / peak_tops, plus gemm_bytes
           ((mk + kn) * in_bytes + mn * out_bytes) for the effective-GB/s metric.
@@ -34,7 +40,7 @@ from teamredbench_amd.native import capi
 from teamredbench_amd.native.runtime import resolve_native_kernel
 from teamredbench_amd.parity import gemm_parity
 from teamredbench_amd.registry import register_benchmark
-from teamredbench_amd.utils import make_tensor, seeded_gemm_operands, timed_iterations
+from teamredbench_amd.utils import seeded_gemm_operands, timed_iterations
 
 DEFAULT_SHAPES = [
     [4096, 4096, 4096],
@@ -141,6 +147,19 @@ class MfuBenchmark(Benchmark):
                 torch.cuda.empty_cache()
         return records
 
+    def _operand_sets(self, spec, m: int, n: int, k: int, out_bytes: int, peak_tops: float | None) -> int:
+        requested = self.params.get("operand_sets", "auto")
+        if requested != "auto":
+            return max(1, int(requested))
+        operand_bytes = (m * k + k * n) * spec.bytes_per_element
+        hbm = self.context.hardware_profile.peak_hbm_bandwidth_gbps
+        if not peak_tops or not hbm or operand_bytes > INFINITY_CACHE_BYTES:
+            return 1
+        intensity = spec.matmul_ops_factor * m * n * k / gemm_bytes(m, n, k, spec.bytes_per_element, out_bytes)
+        if intensity >= peak_tops * 1e12 / (hbm * 1e9):
+            return 1    # compute-bound: where the operands sit does not set the time
+        return min(64, max(3, -(-3 * INFINITY_CACHE_BYTES // operand_bytes)))
+
     def _capi_case(self, lib, torch, spec, peak_tops, m, n, k, case, meta, warmup, iterations, seed, verify,
                    verify_rows) -> BenchmarkRecord:
         device = self.device
@@ -148,6 +167,7 @@ class MfuBenchmark(Benchmark):
         out_dtype = getattr(torch, capi.GEMM_OUTPUT_DTYPES[spec.name])
         c = torch.empty((m, n), device=device, dtype=out_dtype)
         dt = capi.DTYPES[spec.name]
+        sets = self._operand_sets(spec, m, n, k, c.element_size(), peak_tops)
         ws_bytes = lib.gemm_workspace_size(dt, m, n, k)
         ws = torch.empty(ws_bytes, device=device, dtype=torch.uint8) if ws_bytes else None
         stream = torch.cuda.current_stream(device).cuda_stream
@@ -158,14 +178,24 @@ class MfuBenchmark(Benchmark):
                                 stream)
             warmup = max(warmup, int(warmup_s / est) + 1)
             meta["warmup_launches"] = warmup
-        elapsed = lib.time_gemm(dt, a.data_ptr(), b.data_ptr(), c.data_ptr(), m, n, k, sa, sb, ws_ptr, ws_bytes,
-                                warmup, iterations, stream)
-        meta = {**meta, **lib.gemm_info(dt, m, n, k)}
+        if sets > 1:
+            # copies of A, B and C; C of set 0 is the one checked below
+            copies = [(a, b, c)] + [(a.clone(), b.clone(), torch.empty_like(c)) for _ in range(sets - 1)]
+            elapsed = lib.time_gemm_rotating(dt, [x.data_ptr() for x, _, _ in copies],
+                                             [y.data_ptr() for _, y, _ in copies],
+                                             [z.data_ptr() for _, _, z in copies], m, n, k, sa, sb, ws_ptr, ws_bytes,
+                                             warmup, iterations, stream)
+            del copies
+        else:
+            elapsed = lib.time_gemm(dt, a.data_ptr(), b.data_ptr(), c.data_ptr(), m, n, k, sa, sb, ws_ptr, ws_bytes,
+                                    warmup, iterations, stream)
+        meta = {**meta, **lib.gemm_info(dt, m, n, k), "operand_sets": sets}
         if spec.name in capi.FP8_DTYPES:
             meta["scale_a"], meta["scale_b"] = sa, sb
         in_bytes = spec.bytes_per_element
         moved = gemm_bytes(m, n, k, in_bytes, c.element_size())
-        meta["cache_resident_b"] = k * n * in_bytes <= INFINITY_CACHE_BYTES
+        # operands re-read from the Infinity Cache rather than HBM: one set that fits it
+        meta["cache_resident_b"] = sets == 1 and k * n * in_bytes <= INFINITY_CACHE_BYTES
         if verify:
             rows = min(m, verify_rows)
             if spec.name == "float64":
@@ -177,62 +207,63 @@ class MfuBenchmark(Benchmark):
             meta["parity"] = gemm_parity(torch, spec.name, got, ref)
             meta["parity"]["rows_checked"] = rows
             del ref
-        return self.emit_record(
-            BenchmarkRecord(
-                benchmark=self.name,
-                case=case,
-                dtype=spec.name,
-                raw_metrics={
-                    "elapsed_s": elapsed,
-                    "achieved_ops": spec.matmul_ops_factor * m * n * k,
-                    "peak_tops": peak_tops,
-                    "gemm_bytes": moved,
-                },
-                metadata=meta,
-            )
-        )
+        return self.measured(case=case, dtype=spec.name, metadata=meta, raw_metrics={
+            "elapsed_s": elapsed, "achieved_ops": spec.matmul_ops_factor * m * n * k, "peak_tops": peak_tops,
+            "gemm_bytes": moved})
 
     # ------------------------------------------------------------- torch
+    # The reference torch path (mfu.py:183-268): the GEMM through PyTorch's
+    # library kernels (hipBLASLt), timed by wall clock between device
+    # synchronisations (utils.timed_iterations). It runs on the native path's
+    # seeded operands (the reference draws unseeded randn). fp8, which
+    # torch.mm does not take, goes through torch._scaled_mm with the same
+    # per-tensor scales and bf16 output; that routine requires B column-major,
+    # so B is laid out so once, outside the timed region (recorded as b_layout).
+    def _torch_gemm(self, torch, spec, a, b, sa, sb, out):
+        """(callable that runs one GEMM, metadata naming the torch routine)."""
+        if spec.name in capi.FP8_DTYPES:
+            b_cols = b.t().contiguous().t()
+            scale_a = torch.tensor(sa, dtype=torch.float32, device=a.device)
+            scale_b = torch.tensor(sb, dtype=torch.float32, device=a.device)
+            run = lambda: torch._scaled_mm(a, b_cols, scale_a=scale_a, scale_b=scale_b,  # noqa: E731
+                                           out_dtype=torch.bfloat16)
+            return run, {"torch_op": "_scaled_mm", "b_layout": "column_major"}
+        return (lambda: torch.mm(a, b, out=out)), {"torch_op": "mm", "b_layout": "row_major"}
+
     def _run_torch(self) -> list[BenchmarkRecord]:
-        if self.context.torch_module is None:
+        torch = self.context.torch_module
+        if torch is None:
             return [self.skip(case="global", dtype="n/a", error="PyTorch is not installed.")]
-        torch = self.torch
         if not rocm_device_available(torch):
             return [self.skip(case="global", dtype="n/a", error="No ROCm device visible to PyTorch.")]
         self.set_device()
         warmup, iterations, shapes = self._common_params()
+        seed = int(self.params.get("seed", 0))
         records: list[BenchmarkRecord] = []
         for spec in self.selected_dtype_specs():
             peak_tops = self.context.hardware_profile.peak_compute_tops.get(spec.name)
             for shape in shapes:
                 m, n, k = (int(d) for d in shape)
-                case = f"gemm_{m}x{n}x{k}"
-                meta = {"backend": "torch", "m": m, "n": n, "k": k}
+                case, meta = f"gemm_{m}x{n}x{k}", {"backend": "torch", "m": m, "n": n, "k": k}
                 gate = self._gate(spec, peak_tops)
                 if gate:
                     records.append(self.skip(case=case, dtype=spec.name, error=gate, metadata=meta))
                     continue
                 try:
-                    a = make_tensor(torch, spec, (m, k), self.device)
-                    b = make_tensor(torch, spec, (k, n), self.device)
-                    out = torch.empty((m, n), device=self.device, dtype=getattr(torch, spec.torch_attr))
-                    elapsed = timed_iterations(lambda: torch.mm(a, b, out=out), torch_module=torch, warmup=warmup,
-                                               iterations=iterations)
-                except Exception as exc:  # noqa: BLE001 -- any failure skips this case only
+                    a, b, sa, sb = seeded_gemm_operands(torch, m, n, k, spec.name, self.device, seed)
+                    out_dtype = getattr(torch, capi.GEMM_OUTPUT_DTYPES.get(spec.name, spec.torch_attr))
+                    out = torch.empty((m, n), device=self.device, dtype=out_dtype)
+                    gemm, routine = self._torch_gemm(torch, spec, a, b, sa, sb, out)
+                    elapsed = timed_iterations(gemm, torch_module=torch, warmup=warmup, iterations=iterations)
+                except Exception as exc:  # noqa: BLE001 -- a dtype torch cannot multiply skips this case only
                     records.append(self.skip(case=case, dtype=spec.name, error=str(exc), metadata=meta))
                     continue
-                records.append(
-                    self.emit_record(
-                        BenchmarkRecord(
-                            benchmark=self.name,
-                            case=case,
-                            dtype=spec.name,
-                            raw_metrics={"elapsed_s": elapsed, "achieved_ops": spec.matmul_ops_factor * m * n * k,
-                                         "peak_tops": peak_tops},
-                            metadata=meta,
-                        )
-                    )
-                )
+                finally:
+                    torch.cuda.empty_cache()
+                meta.update(routine, timing="wall_clock")
+                records.append(self.measured(case=case, dtype=spec.name, metadata=meta, raw_metrics={
+                    "elapsed_s": elapsed, "achieved_ops": spec.matmul_ops_factor * m * n * k, "peak_tops": peak_tops,
+                    "gemm_bytes": gemm_bytes(m, n, k, spec.bytes_per_element, out.element_size())}))
         return records
 
     def run(self) -> list[BenchmarkRecord]:

@@ -1,9 +1,22 @@
-"""Suite and profile YAML loading (schema of src/teamredbench/config.py:10-150).
+"""Suite and profile files.
 
-A suite names a hardware profile (peaks: the denominators of every % metric),
-a runtime profile, output settings, an optional profiling block, plugin
-modules and a list of benchmark invocations. Profile and output paths are
-resolved relative to the suite file.
+The YAML schema is the reference's (src/teamredbench/config.py:10-150), so a
+suite written for it loads here unchanged:
+
+    name: <suite name>                      # default: the file's stem
+    device:  {profile: <hardware profile yaml>}
+    runtime: {profile: <runtime profile yaml>}
+    outputs: {directory: <dir>, formats: [json, csv]}
+    profiling: {enabled: <bool>, engine: <name>, params: {...}}
+    plugins: [<module>, ...]
+    benchmarks:
+      - {benchmark: <name>, params: {...}, metrics: [<metric>, ...]}
+
+Relative paths are taken from the directory of the file that names them.
+Every value is read through :class:`_Section`, which knows where in which
+file it is, so a malformed file fails with a ``ConfigError`` naming the key
+(``suite.yaml: benchmarks[2].params must be a mapping``) rather than with a
+``KeyError`` or a half-loaded suite.
 """
 from __future__ import annotations
 
@@ -12,6 +25,10 @@ from pathlib import Path
 from typing import Any
 
 import yaml
+
+
+class ConfigError(ValueError):
+    """A suite or profile file that does not follow the schema."""
 
 
 @dataclass
@@ -71,82 +88,140 @@ class SuiteConfig:
     raw: dict[str, Any] = field(default_factory=dict)
 
 
-def _read_mapping(path: Path) -> dict[str, Any]:
-    data = yaml.safe_load(path.read_text(encoding="utf-8")) or {}
-    if not isinstance(data, dict):
-        raise ValueError(f"Expected mapping in {path}")
-    return data
+_MISSING = object()
 
 
-def resolve_relative(base_dir: Path, target: str) -> Path:
-    path = Path(target)
-    return path if path.is_absolute() else (base_dir / path).resolve()
+class _Section:
+    """A mapping read from `origin` at `where` (a dotted key path)."""
+
+    def __init__(self, data: Any, origin: Path, where: str = ""):
+        if not isinstance(data, dict):
+            raise ConfigError(f"{origin.name}: {where or 'the document'} must be a mapping")
+        self.data, self.origin, self.where = data, origin, where
+
+    @classmethod
+    def read(cls, path: Path) -> "_Section":
+        try:
+            data = yaml.safe_load(path.read_text(encoding="utf-8"))
+        except OSError as exc:
+            raise ConfigError(f"cannot read {path}: {exc}") from exc
+        return cls({} if data is None else data, path)
+
+    def _key(self, key: str) -> str:
+        return f"{self.where}.{key}" if self.where else key
+
+    def _fail(self, key: str, what: str) -> ConfigError:
+        return ConfigError(f"{self.origin.name}: {self._key(key)} {what}")
+
+    def get(self, key: str, default: Any = _MISSING) -> Any:
+        value = self.data.get(key, _MISSING)
+        if value is _MISSING or value is None:
+            if default is _MISSING:
+                raise self._fail(key, "is required")
+            return default
+        return value
+
+    def text(self, key: str, default: Any = _MISSING) -> str:
+        value = self.get(key, default)
+        if isinstance(value, (dict, list)):
+            raise self._fail(key, "must be a scalar")
+        return str(value)
+
+    def number(self, key: str) -> float | None:
+        value = self.get(key, None)
+        if value is None:
+            return None
+        try:
+            return float(value)
+        except (TypeError, ValueError):
+            raise self._fail(key, f"must be a number (got {value!r})") from None
+
+    def section(self, key: str) -> "_Section":
+        return _Section(self.get(key, {}), self.origin, self._key(key))
+
+    def mapping(self, key: str, convert=lambda v: v) -> dict[str, Any]:
+        sub = self.section(key)
+        try:
+            return {str(k): convert(v) for k, v in sub.data.items()}
+        except (TypeError, ValueError):
+            raise self._fail(key, "holds a value of the wrong type") from None
+
+    def items(self, key: str) -> list[Any]:
+        value = self.get(key, [])
+        if not isinstance(value, list):
+            raise self._fail(key, "must be a list")
+        return value
+
+    def path(self, key: str, default: Any = _MISSING) -> Path:
+        target = Path(self.text(key, default)).expanduser()
+        return target if target.is_absolute() else (self.origin.parent / target).resolve()
 
 
 def load_hardware_profile(path: Path) -> HardwareProfile:
-    data = _read_mapping(path)
+    """A hardware profile: the peaks every efficiency metric divides by."""
+    doc = _Section.read(Path(path))
     return HardwareProfile(
-        name=str(data["name"]),
-        family=str(data["family"]),
-        peak_hbm_bandwidth_gbps=data.get("peak_hbm_bandwidth_gbps"),
-        peak_link_bandwidth_gbps=dict(data.get("peak_link_bandwidth_gbps") or {}),
-        peak_compute_tops={str(k): float(v) for k, v in (data.get("peak_compute_tops") or {}).items()},
-        notes=list(data.get("notes") or []),
-        path=path,
-        raw=data,
+        name=doc.text("name"),
+        family=doc.text("family"),
+        peak_hbm_bandwidth_gbps=doc.number("peak_hbm_bandwidth_gbps"),
+        peak_link_bandwidth_gbps=doc.mapping("peak_link_bandwidth_gbps"),
+        peak_compute_tops=doc.mapping("peak_compute_tops", float),
+        notes=[str(n) for n in doc.items("notes")],
+        path=Path(path),
+        raw=doc.data,
     )
 
 
 def load_runtime_profile(path: Path) -> RuntimeProfile:
-    data = _read_mapping(path)
+    """A runtime profile: the ROCm stack a run was meant for (recorded, not enforced)."""
+    doc = _Section.read(Path(path))
     return RuntimeProfile(
-        name=str(data["name"]),
-        rocm_version=str(data.get("rocm_version", "unknown")),
-        libraries={str(k): str(v) for k, v in (data.get("libraries") or {}).items()},
-        env={str(k): str(v) for k, v in (data.get("env") or {}).items()},
-        notes=list(data.get("notes") or []),
-        path=path,
-        raw=data,
+        name=doc.text("name"),
+        rocm_version=doc.text("rocm_version", "unknown"),
+        libraries=doc.mapping("libraries", str),
+        env=doc.mapping("env", str),
+        notes=[str(n) for n in doc.items("notes")],
+        path=Path(path),
+        raw=doc.data,
     )
 
 
-def _profiling_config(block: Any, suite_path: Path) -> ProfilingConfig:
-    if block is None:
-        block = {}
-    if not isinstance(block, dict):
-        raise ValueError(f"Expected mapping for profiling config in {suite_path}")
-    engine = block.get("engine")
+def _invocation(doc: _Section, index: int) -> BenchmarkInvocation:
+    entry = _Section(doc.items("benchmarks")[index], doc.origin, f"benchmarks[{index}]")
+    return BenchmarkInvocation(
+        benchmark=entry.text("benchmark"),
+        params=dict(entry.section("params").data),
+        metrics=[str(m) for m in entry.items("metrics")],
+    )
+
+
+def _profiling(doc: _Section) -> ProfilingConfig:
+    block = doc.section("profiling")
+    engine = block.get("engine", None)
     return ProfilingConfig(
-        enabled=bool(block.get("enabled", bool(engine))),
+        # a named engine switches profiling on unless the block says otherwise
+        enabled=bool(block.get("enabled", engine is not None)),
         engine=None if engine is None else str(engine),
-        params=dict(block.get("params") or {}),
-        raw=dict(block),
+        params=dict(block.section("params").data),
+        raw=dict(block.data),
     )
 
 
 def load_suite(path: str | Path) -> SuiteConfig:
     suite_path = Path(path).resolve()
-    data = _read_mapping(suite_path)
-    base = suite_path.parent
-    outputs = data.get("outputs") or {}
+    doc = _Section.read(suite_path)
+    outputs = doc.section("outputs")
     return SuiteConfig(
-        name=str(data.get("name", suite_path.stem)),
-        benchmarks=[
-            BenchmarkInvocation(
-                benchmark=str(item["benchmark"]),
-                params=dict(item.get("params") or {}),
-                metrics=list(item.get("metrics") or []),
-            )
-            for item in data.get("benchmarks") or []
-        ],
-        hardware_profile=load_hardware_profile(resolve_relative(base, str(data["device"]["profile"]))),
-        runtime_profile=load_runtime_profile(resolve_relative(base, str(data["runtime"]["profile"]))),
+        name=doc.text("name", suite_path.stem),
+        benchmarks=[_invocation(doc, i) for i in range(len(doc.items("benchmarks")))],
+        hardware_profile=load_hardware_profile(doc.section("device").path("profile")),
+        runtime_profile=load_runtime_profile(doc.section("runtime").path("profile")),
         outputs=OutputConfig(
-            directory=resolve_relative(base, str(outputs.get("directory", "../../results"))),
-            formats=list(outputs.get("formats", ["json", "csv"])),
+            directory=outputs.path("directory", "../../results"),
+            formats=[str(f) for f in outputs.get("formats", ["json", "csv"])],
         ),
-        profiling=_profiling_config(data.get("profiling"), suite_path),
-        plugins=list(data.get("plugins") or []),
+        profiling=_profiling(doc),
+        plugins=[str(p) for p in doc.items("plugins")],
         path=suite_path,
-        raw=data,
+        raw=doc.data,
     )

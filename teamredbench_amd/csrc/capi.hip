@@ -371,6 +371,33 @@ int mb_time_gemm(int dtype, const void* A, const void* B, void* C, int64_t M, in
         warmup, iterations, st, elapsed_s);
 }
 
+int mb_time_gemm_rotating(int dtype, const void* const* A, const void* const* B, void* const* C, int sets,
+                          int64_t M, int64_t N, int64_t K, float scale_a, float scale_b, void* workspace,
+                          size_t workspace_bytes, int warmup, int iterations, void* stream, double* elapsed_s) {
+    clear_error();
+    if (A == nullptr || B == nullptr || C == nullptr || sets < 1) {
+        set_error("rotating GEMM timing needs operand arrays and sets >= 1 (sets=%d)", sets);
+        return MB_ERR_INVALID_ARG;
+    }
+    const DeviceProps* props = nullptr;
+    int rc = device_for_launch(&props);
+    if (rc != MB_OK) return rc;
+    GemmPlan plan;
+    if ((rc = gemm_plan(dtype, M, N, K, *props, &plan)) != MB_OK) return rc;
+    for (int i = 0; i < sets; ++i)
+        if ((rc = check_gemm_args(dtype, A[i], B[i], C[i], M, N, K, workspace, workspace_bytes, plan)) != MB_OK)
+            return rc;
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    int next = 0;
+    return timed_loop(
+        [&]() {
+            const int i = next;
+            next = next + 1 == sets ? 0 : next + 1;
+            return gemm_launch(dtype, A[i], B[i], C[i], M, N, K, scale_a, scale_b, workspace, plan, st);
+        },
+        warmup, iterations, st, elapsed_s);
+}
+
 int mb_kernel_info(int kind, int a, int b, int64_t m, int64_t n, int64_t k, char* json, size_t cap) {
     clear_error();
     const DeviceProps* props = nullptr;

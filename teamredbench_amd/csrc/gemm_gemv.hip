@@ -183,6 +183,8 @@ int gemm_gemv_plan(int dtype, int64_t M, int64_t N, int64_t K, const DeviceProps
     int64_t splits = 1;
     while (groups * splits * 2 <= 2 * cus && K / (splits * 2) >= kGvChunk * kGvHalfWaves && splits < 1024)
         splits *= 2;
+    const int64_t force_splits = tuning(MB_TUNE_GEMM_SPLITS);
+    if (force_splits >= 1) splits = force_splits;
     if (splits > 65535) splits = 65535;
     plan->implementation = "gfx950_gemv_stream";
     plan->threads = kGvThreads;

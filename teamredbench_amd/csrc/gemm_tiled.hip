@@ -559,10 +559,11 @@ gemm_tiled_kernel(const unsigned char* __restrict__ A, const unsigned char* __re
     // fills only one 8-byte half of every chunk. Rows at or past M (a
     // partial last tile) are not stored. With K splits the block writes its
     // unscaled fp32 partial to ws[split][row][col] directly; a second kernel
-    // sums the splits.
+    // sums the splits. Plans split only tiles of at most 128 rows, so the
+    // 256-row kernels leave that path out (its registers spilled there).
     const int row0 = tm * BM + wm * WTM + (lane & 31);
     const int64_t col0 = (int64_t)tn * BN + wn * WTN + 4 * half;
-    if (ws == nullptr) {
+    if (BM > 128 || ws == nullptr) {
         constexpr int ROW_BYTES = WTN * 2;
         constexpr int ROW_CHUNKS = ROW_BYTES / 16;
         static_assert(ROW_CHUNKS == 16 || ROW_CHUNKS == 8, "staging covers wave tiles 128 or 64 columns wide");
@@ -594,7 +595,7 @@ gemm_tiled_kernel(const unsigned char* __restrict__ A, const unsigned char* __re
         };
         stage_tile(std::integral_constant<bool, SCALED>{});
         store_staged_tile<WTM, ROW_BYTES>(stage, C, M, N, tm * BM + wm * WTM, (int64_t)tn * BN + wn * WTN, lane);
-    } else {
+    } else if constexpr (BM <= 128) {
         float* part = ws + (int64_t)split * M * N;
 #pragma unroll
         for (int i = 0; i < FM; ++i) {
@@ -900,8 +901,9 @@ gemm_fp8_mi16_kernel(const unsigned char* __restrict__ A, const unsigned char* _
     // C[16i + l % 16][16j + 4(l / 16) + r]: four consecutive columns of one
     // row, rounded to 16 bits into the wave's LDS staging rows and stored as
     // whole row segments (store_staged_tile). With K splits the block writes
-    // its unscaled fp32 partial to ws[split][row][col] instead.
-    if (ws == nullptr) {
+    // its unscaled fp32 partial to ws[split][row][col] instead (tiles of at
+    // most 128 rows only).
+    if (BM > 128 || ws == nullptr) {
         constexpr int ROW_BYTES = WTN * 2;
         constexpr int ROW_CHUNKS = ROW_BYTES / 16;
         static_assert(ROW_CHUNKS == 16 || ROW_CHUNKS == 8, "staging covers wave tiles 128 or 64 columns wide");
@@ -921,7 +923,7 @@ gemm_fp8_mi16_kernel(const unsigned char* __restrict__ A, const unsigned char* _
             }
         }
         store_staged_tile<WTM, ROW_BYTES>(stage, C, M, N, tm * BM + wm * WTM, (int64_t)tn * BN + wn * WTN, lane);
-    } else {
+    } else if constexpr (BM <= 128) {
         float* part = ws + (int64_t)split * M * N;
         const int row0 = tm * BM + wm * WTM + l16;
         const int64_t col0 = (int64_t)tn * BN + wn * WTN + 4 * g;
@@ -1040,11 +1042,10 @@ int gemm_tiled_plan(int dtype, int64_t M, int64_t N, int64_t K, const DeviceProp
     }
     const int64_t cus = props.cu_count > 0 ? props.cu_count : 256;
     auto tiles = [&](int i) { return ((M + kConfigs[i].bm - 1) / kConfigs[i].bm) * (N / kConfigs[i].bn); };
-    int cfg = (int)tuning(MB_TUNE_GEMM_TILED_CONFIG);  // -1 unless forced
-    const bool config_forced = cfg >= 0;
-    if (n128_only && cfg != 3) cfg = 2;
-    const bool forced = cfg >= 0;
-    if (cfg < 0) cfg = (tiles(0) >= cus && M % kConfigs[0].bm == 0) ? 0 : 1;
+    const int forced_cfg = (int)tuning(MB_TUNE_GEMM_TILED_CONFIG);  // -1 unless forced
+    // N % 256 != 0 leaves the 128-column tiles (configurations 2 and 3).
+    const int pinned = forced_cfg >= 0 && n128_only && forced_cfg < 2 ? 2 : forced_cfg;
+    int cfg = pinned >= 0 ? pinned : (!n128_only && tiles(0) >= cus && M % kConfigs[0].bm == 0) ? 0 : -1;
     // Last-round fill. 128 x 256 tiles run 7-14% below 256 x 256 per FLOP on
     // MI355X, and a partly filled last round costs less than a full one (the
     // busy CUs clock up under the power limit), so the smaller tile pays only
@@ -1053,75 +1054,65 @@ int gemm_tiled_plan(int dtype, int64_t M, int64_t N, int64_t K, const DeviceProp
     // 6144^3 1-5%, while 2.5- and 3.5-round shapes ran 3-15% slower.
     // Such shapes have at least one tile per CU: no K split.
     bool fill_rule = false;
-    if (!forced && cfg == 0) {
+    if (pinned < 0 && cfg == 0) {
         const int64_t full = tiles(0) / cus, rest = tiles(0) % cus;
         fill_rule = full <= 2 && rest > 0 && 4 * rest <= cus;
         if (fill_rule) cfg = 1;
     }
-    // K splits for problems with too few tiles to fill the GPU, chosen by a
-    // cost model whose four constants were fitted to a sweep on MI355X (bf16
-    // and fp8 e4m3; M = 16..8192, N = 1024..16384, K = 2048..16384; every
-    // power-of-two split timed): it picks the measured best split or one
-    // within 3% on 49 of 52 shapes, 12% at worst. Per split count s:
-    //   MFMA:    rounds of blocks x one block's 2*BM*BN*K/s FLOP at ~6 TFLOP/s
-    //            per CU for 16-bit inputs (twice that for fp8);
-    //   stream:  the A and B bytes at ~5 TB/s, slowed by sqrt(s * N * elem /
-    //            64 KiB) once the B row bytes the splits read at once pass
-    //            64 KiB (each split reads its own K rows; more concurrent row
-    //            positions cost DRAM page locality: 16 x 8192 x 8192 bf16 runs
-    //            26 us at 4 splits and 31 us at 16);
-    //   partials (s > 1): the fp32 partials written and read back,
-    //            2 * s * M * N * 4 bytes at ~5 TB/s, plus ~5 us for the
-    //            reduction's launch.
-    // time(s) = max(MFMA, stream) + partials; the smallest time wins. The
-    // model rates both 128-row configurations, 128 x 256 and 128 x 128 tiles
-    // (twice the blocks for the same B traffic: skinny and few-tile shapes
-    // fill the CUs with fewer K splits), keeping 128 x 256 on a tie. Against
-    // the previous choice of 128 x 256 tiles alone it ran every bf16 shape it
-    // changes faster on MI355X (16..256 x 8192 x 8192 by 2-7%, 128 x 4096 x
-    // 4096 by 21%, 256 x 512 x 1024 by 34%) and 12 of 13 fp8 shapes (up to
-    // 30%; 16 x 8192 x 8192 fp8 5% slower).
+    // Problems with too few 256 x 256 tiles to fill the GPU: the tile
+    // configuration (128 x 256, 128 x 128 or 64 x 128) and the K split count s
+    // (1, 2, 4 .. 32, whole stages per split) that a cost model rates fastest:
+    //   blocks  = tiles * s, in ceil(blocks / CUs) rounds;
+    //   MFMA    = rounds x one block's 2 * BM * BN * K / s FLOP at a per-CU
+    //             rate of the configuration (4.57 / 3.67 / 2.64 TFLOP/s for
+    //             16-bit inputs, twice that for fp8);
+    //   stream  = the A and B bytes at 9.16 TB/s times the fraction of the
+    //             CUs the blocks occupy (each block keeps a fixed number of
+    //             loads in flight, so too few blocks leave HBM idle);
+    //   partials (s > 1): the fp32 partials written and read back at the
+    //             same rate, plus 7.1 us for the reduction pass;
+    //   time    = max(MFMA, stream) + rounds x 3.0 us (prologue, epilogue)
+    //             + partials.
+    // The constants were fitted to 666 timings on MI355X (bf16, fp16, fp8
+    // e4m3; 45 shapes, M = 8..4096, N = 256..16384, K = 768..16384; every
+    // configuration x split 1..16) with B cycled through copies that exceed
+    // the 256 MB Infinity Cache, i.e. operands streamed from HBM. The
+    // model's pick is within 1.8% of the measured best in geometric mean
+    // (20% at worst); the previous model, fitted with B cache-resident,
+    // ran those shapes 9.7% (44% at worst) behind. 16 x 8192 x 8192 bf16:
+    // 4 splits on 128 x 128 tiles, 29.2 us against 35.5 for its 2.
     int splits = 1;
-    if (kConfigs[cfg].bm == 128 && !fill_rule) {
-        const int cands[2] = {cfg, 2};
-        const int n_cands = (!forced && cfg == 1) ? 2 : 1;
-        const double flops_per_cu = 6.0e12 * (e == 1 ? 2.0 : 1.0), bw = 5.0e12;
+    if (!fill_rule && (cfg < 0 || kConfigs[cfg].bm <= 128)) {
+        constexpr double kRate[4] = {0.0, 4.57e12, 3.67e12, 2.64e12}, kBw = 9.16e12, kRound = 2.99e-6,
+                         kReduce = 7.11e-6;
+        int cands[3] = {1, 2, 3}, n_cands = 3, first = 0;
+        if (cfg >= 0) cands[0] = cfg, n_cands = 1;
+        else if (n128_only) first = 1;
         double best = -1.0;
-        int best_cfg = cfg;
-        for (int ci = 0; ci < n_cands; ++ci) {
+        for (int ci = first; ci < n_cands; ++ci) {
             const int c = cands[ci];
             const double bm = kConfigs[c].bm, bn = kConfigs[c].bn;
-            for (int64_t s = 1; s <= 32; s *= 2) {
-                if (K % (stage_k * s) != 0) continue;
-                const double rounds = (double)((tiles(c) * s + cus - 1) / cus);
-                const double mfma = rounds * 2.0 * bm * bn * ((double)K / (double)s) / flops_per_cu;
-                const double rows_in_flight = (double)(s * N * e) / 65536.0;
-                const double stream =
-                    (double)((K * N + M * K) * e) / bw * std::sqrt(rows_in_flight > 1.0 ? rows_in_flight : 1.0);
-                const double partials = s > 1 ? 2.0 * (double)s * (double)M * (double)N * 4.0 / bw + 5.0e-6 : 0.0;
-                const double t = (mfma > stream ? mfma : stream) + partials;
+            const double rate = kRate[c] * (e == 1 ? 2.0 : 1.0);
+            for (int64_t sp = 1; sp <= 32; sp *= 2) {
+                if (K % (stage_k * sp) != 0) continue;
+                const double blocks = (double)(tiles(c) * sp);
+                const double rounds = std::ceil(blocks / (double)cus);
+                const double mfma = rounds * 2.0 * bm * bn * ((double)K / (double)sp) / rate;
+                const double occupancy = blocks < (double)cus ? blocks / (double)cus : 1.0;
+                const double stream = (double)((K * N + M * K) * e) / (kBw * occupancy);
+                const double partials = sp > 1 ? 2.0 * (double)sp * (double)M * (double)N * 4.0 / kBw + kReduce : 0.0;
+                const double t = (mfma > stream ? mfma : stream) + rounds * kRound + partials;
                 if (best < 0.0 || t < best) {
                     best = t;
-                    best_cfg = c;
-                    splits = (int)s;
+                    cfg = c;
+                    splits = (int)sp;
                 }
             }
         }
-        cfg = best_cfg;
     }
-    // 64 x 128 tiles for problems the 128 x 128 plan leaves with few blocks:
-    // at the same split count they halve each block's MFMA work and double
-    // the blocks. Taken when the doubled count still fits in half the CUs:
-    // on MI355X 1024^3 ran 22% faster, 640 x 1536 x 768 19%, 100 x 2048 x 4096
-    // 17%, 512 x 256 x 4096 15% (bf16 and fp8 alike); with more blocks than
-    // that the narrower tile lost (3072^3 7-11% slower, 2048^3 27-55%), except
-    // for bf16 and fp8 problems of one 128-row tile, up to one block per CU
-    // (128 x 8192 x 8192 at 2 splits: bf16 2.5-9.5%, fp8 9%; fp16 ran 4-7%
-    // slower at 128 x 8192 x 8192 and 128 x 4096 x 4096, so it keeps 128 x 128).
-    const bool one_tile_rule = dtype != MB_DT_FLOAT16 && M <= kConfigs[2].bm && tiles(3) * splits <= cus;
-    if (!config_forced && cfg == 2 && (tiles(3) * splits * 2 <= cus || one_tile_rule)) cfg = 3;
     const int64_t force_splits = tuning(MB_TUNE_GEMM_SPLITS);
     if (force_splits >= 1 && K % (stage_k * force_splits) == 0) splits = (int)force_splits;
+    if (kConfigs[cfg].bm > 128) splits = 1;   // the 256-row kernels carry no split path
     if (tiles(cfg) * splits > INT32_MAX) {
         *why = "more than 2^31 tiles";
         return MB_ERR_SHAPE;

@@ -1,85 +1,103 @@
-"""Result writers: JSON records, flattened CSV and the metadata sidecar
-(formats of src/teamredbench/io.py:12-87; sidecar schema_version 1)."""
+"""Result files of a suite run.
+
+Three files share one stem, ``<suite>-<UTC timestamp>``, in the output
+directory: ``.json`` (a list of record objects), ``.csv`` (one flat row per
+record) and ``.metadata.json`` (the sidecar: schema_version 1, counts by
+status, the paths written, and the run's provenance under ``run``). These
+are the reference's formats (src/teamredbench/io.py:12-87) -- tools that read
+its results read these. The record forms themselves are
+``BenchmarkRecord.to_dict`` / ``to_row``. The sidecar is always written;
+JSON and CSV only when the suite's ``outputs.formats`` asks for them, and a
+format this writer does not know is listed in the sidecar under
+``ignored_formats`` instead of failing the run after its measurements.
+"""
 from __future__ import annotations
 
+from collections import Counter
 import csv
 from datetime import datetime, timezone
 import json
 from pathlib import Path
-from typing import Iterable
+from typing import Any, Callable, Iterable
 
 from teamredbench_amd.benchmarks.base import BenchmarkRecord
 
-
-def record_to_dict(record: BenchmarkRecord) -> dict[str, object]:
-    return {
-        "benchmark": record.benchmark,
-        "case": record.case,
-        "dtype": record.dtype,
-        "status": record.status,
-        "error": record.error,
-        "metrics": record.metrics,
-        "raw_metrics": record.raw_metrics,
-        "metadata": record.metadata,
-    }
+SIDECAR_SCHEMA_VERSION = 1
 
 
-def record_to_row(record: BenchmarkRecord) -> dict[str, object]:
-    row: dict[str, object] = {
-        "benchmark": record.benchmark,
-        "case": record.case,
-        "dtype": record.dtype,
-        "status": record.status,
-        "error": record.error or "",
-    }
-    for prefix, mapping in (("metric", record.metrics), ("raw", record.raw_metrics), ("meta", record.metadata)):
-        for key in sorted(mapping):
-            value = mapping[key]
-            row[f"{prefix}_{key}"] = json.dumps(value) if isinstance(value, (dict, list)) else value
-    return row
+def _utc_stamp(moment: datetime) -> str:
+    return moment.strftime("%Y%m%dT%H%M%SZ")
 
 
-def write_results(
-    records: Iterable[BenchmarkRecord],
-    suite_name: str,
-    output_dir: Path,
-    formats: list[str],
-    run_metadata: dict[str, object] | None = None,
-) -> dict[str, Path]:
-    records = list(records)
-    output_dir.mkdir(parents=True, exist_ok=True)
-    stamp = datetime.now(timezone.utc).strftime("%Y%m%dT%H%M%SZ")
-    stem = output_dir / f"{suite_name}-{stamp}"
-    outputs: dict[str, Path] = {}
+def _iso_utc(moment: datetime) -> str:
+    return moment.isoformat().replace("+00:00", "Z")
 
-    if "json" in formats:
-        path = stem.with_name(stem.name + ".json")
-        path.write_text(json.dumps([record_to_dict(r) for r in records], indent=2), encoding="utf-8")
-        outputs["json"] = path
 
-    if "csv" in formats:
-        path = stem.with_name(stem.name + ".csv")
-        rows = [record_to_row(r) for r in records]
-        columns = sorted({key for row in rows for key in row})
-        with path.open("w", encoding="utf-8", newline="") as handle:
+class ResultWriter:
+    """Writes one run's records under ``<output_dir>/<suite>-<stamp>.*``."""
+
+    def __init__(self, output_dir: Path, suite_name: str, now: datetime | None = None):
+        self.output_dir = Path(output_dir)
+        self.created = now or datetime.now(timezone.utc)
+        self.stem = f"{suite_name}-{_utc_stamp(self.created)}"
+        self.suite_name = suite_name
+
+    def path(self, suffix: str) -> Path:
+        return self.output_dir / f"{self.stem}{suffix}"
+
+    def write_json(self, records: list[BenchmarkRecord]) -> Path:
+        target = self.path(".json")
+        target.write_text(json.dumps([r.to_dict() for r in records], indent=2), encoding="utf-8")
+        return target
+
+    def write_csv(self, records: list[BenchmarkRecord]) -> Path:
+        target = self.path(".csv")
+        rows = [r.to_row() for r in records]
+        columns = sorted(set().union(*rows)) if rows else ["benchmark", "case", "dtype", "error", "status"]
+        with target.open("w", encoding="utf-8", newline="") as handle:
             writer = csv.DictWriter(handle, fieldnames=columns)
             writer.writeheader()
             writer.writerows(rows)
-        outputs["csv"] = path
+        return target
 
-    meta_path = stem.with_name(stem.name + ".metadata.json")
-    outputs["metadata"] = meta_path
-    counts: dict[str, int] = {}
-    for record in records:
-        counts[record.status] = counts.get(record.status, 0) + 1
-    payload = {
-        "schema_version": 1,
-        "suite_name": suite_name,
-        "generated_at_utc": datetime.now(timezone.utc).isoformat().replace("+00:00", "Z"),
-        "record_count": len(records),
-        "record_status_counts": counts,
-        "outputs": {name: str(path) for name, path in outputs.items()},
-        "run": run_metadata or {},
+    WRITERS: dict[str, Callable[["ResultWriter", list[BenchmarkRecord]], Path]] = {
+        "json": write_json,
+        "csv": write_csv,
     }
-    meta_path.write_text(json.dumps(payload, indent=2), encoding="utf-8")
-    return outputs
+
+    def write(self, records: Iterable[BenchmarkRecord], formats: list[str],
+              run_metadata: dict[str, Any] | None = None) -> dict[str, Path]:
+        records = list(records)
+        self.output_dir.mkdir(parents=True, exist_ok=True)
+        outputs = {fmt: self.WRITERS[fmt](self, records) for fmt in self.WRITERS if fmt in formats}
+        outputs["metadata"] = self.path(".metadata.json")
+        sidecar: dict[str, Any] = {
+            "schema_version": SIDECAR_SCHEMA_VERSION,
+            "suite_name": self.suite_name,
+            "generated_at_utc": _iso_utc(datetime.now(timezone.utc)),
+            "record_count": len(records),
+            "record_status_counts": dict(Counter(r.status for r in records)),
+            "outputs": {name: str(path) for name, path in outputs.items()},
+            "run": run_metadata or {},
+        }
+        unknown = [fmt for fmt in formats if fmt not in self.WRITERS]
+        if unknown:
+            sidecar["ignored_formats"] = unknown
+        outputs["metadata"].write_text(json.dumps(sidecar, indent=2), encoding="utf-8")
+        return outputs
+
+
+def write_results(records: Iterable[BenchmarkRecord], suite_name: str, output_dir: Path, formats: list[str],
+                  run_metadata: dict[str, object] | None = None) -> dict[str, Path]:
+    """Write the result files of one run; returns {"json"|"csv"|"metadata": path}."""
+    return ResultWriter(output_dir, suite_name).write(records, formats, run_metadata)
+
+
+def read_results(sidecar_path: Path) -> tuple[dict[str, Any], list[BenchmarkRecord]]:
+    """The sidecar of a run and the records of the JSON file it names."""
+    sidecar = json.loads(Path(sidecar_path).read_text(encoding="utf-8"))
+    json_path = sidecar.get("outputs", {}).get("json")
+    if json_path is None or not Path(json_path).exists():
+        raise FileNotFoundError(f"{sidecar_path} names no JSON results file")
+    payload = json.loads(Path(json_path).read_text(encoding="utf-8"))
+    return sidecar, [BenchmarkRecord.from_dict(item) for item in payload]

@@ -105,6 +105,14 @@ SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
             ctypes.c_size_t, ctypes.c_int, ctypes.c_int, _vp, ctypes.POINTER(ctypes.c_double),
         ],
     ),
+    "mb_time_gemm_rotating": (
+        ctypes.c_int,
+        [
+            ctypes.c_int, ctypes.POINTER(_cvp), ctypes.POINTER(_cvp), ctypes.POINTER(_vp), ctypes.c_int, _i64, _i64,
+            _i64, ctypes.c_float, ctypes.c_float, _vp, ctypes.c_size_t, ctypes.c_int, ctypes.c_int, _vp,
+            ctypes.POINTER(ctypes.c_double),
+        ],
+    ),
     "mb_kernel_info": (
         ctypes.c_int,
         [ctypes.c_int, ctypes.c_int, ctypes.c_int, _i64, _i64, _i64, ctypes.c_char_p, ctypes.c_size_t],
@@ -180,6 +188,22 @@ class NativeLibrary:
             int(warmup), int(iterations), stream or None, ctypes.byref(out),
         )
         self._check(status, "mb_time_gemm")
+        return out.value
+
+    def time_gemm_rotating(self, dtype: int, a: list[int], b: list[int], c: list[int], m: int, n: int, k: int,
+                           scale_a: float, scale_b: float, workspace: int | None, workspace_bytes: int, warmup: int,
+                           iterations: int, stream: int | None = None) -> float:
+        """mb_time_gemm cycling over len(a) operand sets (a[i], b[i] -> c[i])."""
+        sets = len(a)
+        if not sets or len(b) != sets or len(c) != sets:
+            raise ValueError("operand lists must be non-empty and of equal length")
+        arrays = [(ctypes.c_void_p * sets)(*ptrs) for ptrs in (a, b, c)]
+        out = ctypes.c_double(0.0)
+        status = self.handle.mb_time_gemm_rotating(
+            dtype, *arrays[:3], sets, m, n, k, float(scale_a), float(scale_b), workspace or None,
+            int(workspace_bytes), int(warmup), int(iterations), stream or None, ctypes.byref(out),
+        )
+        self._check(status, "mb_time_gemm_rotating")
         return out.value
 
     # ---- metadata ----------------------------------------------------------

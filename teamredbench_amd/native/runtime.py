@@ -1,21 +1,31 @@
-"""Resolution of ``params.native`` and the external-executable contract.
+"""``params.native``: which native kernel a benchmark runs, and how.
 
-``resolve_native_kernel`` reads ``params.native.{kernel, source, binary,
-compiler, compile_args, run_args, env, cache_dir}`` exactly as the reference
-does (src/teamredbench/native/runtime.py:65-119); relative paths resolve
-against the suite file.
+Selection (the keys of src/teamredbench/native/runtime.py:65-119, so suites
+written for the reference resolve the same way):
+  params.native.kernel        a registered name (default: the benchmark's
+                              built-in, e.g. ``hbm_hip`` -> the gfx950 stream
+                              kernels of libmi355bench.so)
+  params.native.source        a HIP source to build (overrides the kernel's)
+  params.native.binary        a ready executable (no build)
+  params.native.compiler / compile_args / run_args / env / cache_dir
+Relative paths are taken from the suite file's directory.
 
-Built-in kernels (abi "capi") need nothing more: the benchmark calls
-libmi355bench.so through :mod:`teamredbench_amd.native.capi`. A
-user-supplied ``source`` or ``binary`` -- or a plugin kernel registered with
-abi "executable" -- keeps the reference's process contract
-(docs/extending.md:155-175): hipcc builds the source into a cache keyed by a
-sha256 over the source, its local ``#include "..."`` closure, the compiler
-and the flags; the executable receives argv and its last non-empty stdout
-line must be a JSON object ``{status, raw_metrics, metadata, error}``.
+Built-in kernels (abi "capi") run in-process through the C ABI
+(:mod:`teamredbench_amd.native.capi`). A user ``source`` or ``binary``, or
+a plugin registered with abi "executable", keeps the reference's process
+contract: argv in, and the last non-empty stdout line is a JSON object
+``{status, raw_metrics, metadata, error}`` (docs/extending.md:155-175).
+
+Sources are built by :class:`KernelCache`: one executable per content key,
+a sha256 over the source, every local ``#include "..."`` it reaches (so
+editing a header rebuilds), the compiler and the flags. Builds target
+gfx950 (``--offload-arch=gfx950``) unless the flags name an offload arch,
+and land under a temporary name first, so an interrupted build never leaves
+a truncated executable under its final name.
 """
 from __future__ import annotations
 
+from collections import deque
 from dataclasses import dataclass, field
 import hashlib
 import json
@@ -26,7 +36,10 @@ import shutil
 import subprocess
 from typing import Any
 
+from teamredbench_amd.config import ConfigError, _Section
 from teamredbench_amd.native.registry import ABI_CAPI, ABI_EXECUTABLE, get_native_kernel
+
+DEFAULT_OFFLOAD_ARCH = "gfx950"
 
 
 class NativeKernelError(RuntimeError):
@@ -59,145 +72,178 @@ class NativeKernelResult:
     metadata: dict[str, Any]
     error: str | None = None
 
+    @classmethod
+    def from_stdout(cls, stdout: str) -> "NativeKernelResult":
+        """The contract line: the last non-empty line of the executable's stdout."""
+        line = next((text.strip() for text in reversed(stdout.splitlines()) if text.strip()), None)
+        if line is None:
+            raise NativeKernelError("Native kernel produced no JSON output.")
+        try:
+            payload = json.loads(line)
+        except json.JSONDecodeError as exc:
+            raise NativeKernelError(f"Native kernel output was not valid JSON: {exc}") from exc
+        if not isinstance(payload, dict):
+            raise NativeKernelError("Native kernel output JSON must be an object.")
+        parts = {}
+        for key in ("raw_metrics", "metadata"):
+            value = payload.get(key, {})
+            if not isinstance(value, dict):
+                raise NativeKernelError(f"Native kernel {key} must be a JSON object.")
+            parts[key] = dict(value)
+        error = payload.get("error")
+        return cls(status=str(payload.get("status", "ok")), error=None if error is None else str(error), **parts)
 
-def _as_str_list(value: Any, label: str) -> list[str]:
-    if value is None:
-        return []
-    if not isinstance(value, list):
-        raise ValueError(f"{label} must be a list of strings.")
-    return [str(v) for v in value]
+
+def parse_native_result(stdout: str) -> NativeKernelResult:
+    return NativeKernelResult.from_stdout(stdout)
 
 
-def _as_str_map(value: Any, label: str) -> dict[str, str]:
-    if value is None:
-        return {}
-    if not isinstance(value, dict):
-        raise ValueError(f"{label} must be a mapping.")
-    return {str(k): str(v) for k, v in value.items()}
+def _string_list(block: _Section, key: str) -> list[str]:
+    values = block.get(key, [])
+    if not isinstance(values, list):
+        raise ConfigError(f"{block.origin.name}: {block.where}.{key} must be a list of strings.")
+    return [str(v) for v in values]
 
 
-def _user_path(base: Path, value: str) -> Path:
-    path = Path(value)
-    return path if path.is_absolute() else (base / path).resolve()
-
-
-def resolve_native_kernel(
-    *,
-    benchmark: str,
-    params: dict[str, Any],
-    suite_path: Path | None,
-    repo_root: Path | None,
-    default_kernel: str | None = None,
-) -> ResolvedNativeKernel:
-    native = params.get("native") or {}
-    if not isinstance(native, dict):
-        raise ValueError("benchmark params.native must be a mapping.")
+def resolve_native_kernel(*, benchmark: str, params: dict[str, Any], suite_path: Path | None,
+                          repo_root: Path | None, default_kernel: str | None = None) -> ResolvedNativeKernel:
     base = suite_path.parent if suite_path else (repo_root or Path.cwd())
+    origin = suite_path or base / "params"
+    if not isinstance(params.get("native") or {}, dict):
+        raise ConfigError(f"{origin.name}: benchmark params.native must be a mapping.")
+    block = _Section(params.get("native") or {}, origin, "params.native")   # paths resolve against `base`
 
-    kernel_name = str(native.get("kernel", default_kernel or "")).strip() or None
-    definition = get_native_kernel(kernel_name) if kernel_name else None
+    name = str(block.get("kernel", default_kernel or "")).strip() or None
+    definition = get_native_kernel(name) if name else None
     if definition is not None and definition.benchmark != benchmark:
         raise ValueError(f"Native kernel {definition.name} is registered for {definition.benchmark}, not {benchmark}.")
-
-    source = definition.source_path if definition is not None else None
-    binary = _user_path(base, str(native["binary"])) if native.get("binary") else None
-    user_source = _user_path(base, str(native["source"])) if native.get("source") else None
-    if user_source is not None:
-        source = user_source
-    # A user-supplied source or binary always goes through the executable contract.
-    abi = definition.abi if definition is not None and binary is None and user_source is None else ABI_EXECUTABLE
-
-    compile_args = list(definition.compile_args if definition is not None else ())
-    compile_args += _as_str_list(native.get("compile_args"), "native.compile_args")
+    user_source = block.path("source") if block.get("source", None) else None
+    binary = block.path("binary") if block.get("binary", None) else None
+    source = user_source or (definition.source_path if definition is not None else None)
+    # a user-supplied source or binary always goes through the executable contract
+    abi = definition.abi if definition is not None and user_source is None and binary is None else ABI_EXECUTABLE
     if abi == ABI_EXECUTABLE and source is None and binary is None:
-        if kernel_name is None:
-            raise ValueError(
-                "No native kernel configured. Set params.native.kernel, params.native.source, or params.native.binary."
-            )
-        raise ValueError(f"Native kernel {kernel_name} does not define a source or binary path.")
-
+        raise ValueError("No native kernel configured. Set params.native.kernel, params.native.source, or "
+                         "params.native.binary." if name is None else
+                         f"Native kernel {name} does not define a source or binary path.")
     if definition is not None and abi == ABI_CAPI:
-        name = definition.name
+        resolved_name = definition.name
     else:
-        name = kernel_name or (source.stem if source is not None else binary.stem)
+        resolved_name = name or (source or binary).stem
+    env = block.get("env", {})
+    if not isinstance(env, dict):
+        raise ConfigError(f"{origin.name}: params.native.env must be a mapping.")
     return ResolvedNativeKernel(
         benchmark=benchmark,
-        name=name,
+        name=resolved_name,
         description=definition.description if definition is not None else "external native kernel",
         source_path=source,
         binary_path=binary,
-        compiler=str(native["compiler"]) if native.get("compiler") else None,
-        compile_args=tuple(compile_args),
-        run_args=tuple(_as_str_list(native.get("run_args"), "native.run_args")),
-        env=_as_str_map(native.get("env"), "native.env"),
-        cache_dir=_user_path(base, str(native["cache_dir"])) if native.get("cache_dir") else None,
+        compiler=block.text("compiler") if block.get("compiler", None) else None,
+        compile_args=tuple((definition.compile_args if definition is not None else ()) +
+                           tuple(_string_list(block, "compile_args"))),
+        run_args=tuple(_string_list(block, "run_args")),
+        env={str(k): str(v) for k, v in env.items()},
+        cache_dir=block.path("cache_dir") if block.get("cache_dir", None) else None,
         abi=abi,
     )
 
 
-# ------------------------------------------------------------------ cache
+# ------------------------------------------------------------------ builds
 def native_cache_dir(explicit: Path | None = None) -> Path:
+    """Where external kernels are built: ``$XDG_CACHE_HOME/teamredbench/native`` (or ~/.cache/...)."""
     if explicit is not None:
-        return explicit
-    xdg = os.environ.get("XDG_CACHE_HOME")
-    root = Path(xdg).expanduser().resolve() if xdg else Path.home().resolve() / ".cache"
-    return root / "teamredbench" / "native"
-
-
-def clear_native_cache(explicit: Path | None = None) -> tuple[Path, int]:
-    cache = native_cache_dir(explicit)
-    if not cache.exists():
-        return cache, 0
-    removed = 0
-    for entry in cache.iterdir():
-        if entry.is_dir():
-            shutil.rmtree(entry)
-        else:
-            entry.unlink()
-        removed += 1
-    return cache, removed
+        return Path(explicit)
+    root = os.environ.get("XDG_CACHE_HOME")
+    return (Path(root).expanduser() if root else Path.home() / ".cache").resolve() / "teamredbench" / "native"
 
 
 def _find_hip_compiler(preferred: str | None = None) -> str:
-    for candidate in (
-        preferred,
-        os.environ.get("TEAMREDBENCH_HIPCC"),
-        "hipcc",
-        "/opt/rocm/bin/hipcc",
-        "amdclang++",
-        "/opt/rocm/bin/amdclang++",
-    ):
+    for candidate in (preferred, os.environ.get("TEAMREDBENCH_HIPCC"), "hipcc", "/opt/rocm/bin/hipcc",
+                      "amdclang++", "/opt/rocm/bin/amdclang++"):
         if not candidate:
             continue
-        if Path(candidate).is_absolute():
-            if Path(candidate).exists():
-                return candidate
-            continue
-        found = shutil.which(candidate)
+        path = Path(candidate)
+        found = str(path) if path.is_absolute() and path.exists() else (None if path.is_absolute()
+                                                                       else shutil.which(candidate))
         if found:
             return found
-    raise NativeKernelError("No HIP compiler found. Set TEAMREDBENCH_HIPCC, params.native.compiler, or params.native.binary.")
+    raise NativeKernelError("No HIP compiler found. Set TEAMREDBENCH_HIPCC, params.native.compiler, or "
+                            "params.native.binary.")
 
 
-_INCLUDE = re.compile(r'^\s*#\s*include\s*"([^"]+)"', re.MULTILINE)
+_LOCAL_INCLUDE = re.compile(r'^\s*#\s*include\s*"([^"]+)"', re.MULTILINE)
 
 
-def _hash_sources(digest: "hashlib._Hash", path: Path, seen: set[Path]) -> None:
-    """Feed `path` and, depth-first, every local include that exists into `digest`."""
-    path = path.resolve()
-    if path in seen:
-        return
-    seen.add(path)
-    data = path.read_bytes()
-    digest.update(str(path).encode() + b"\0" + data)
-    for name in _INCLUDE.findall(data.decode("utf-8", errors="ignore")):
-        candidate = (path.parent / name).resolve()
-        if candidate.exists():
-            _hash_sources(digest, candidate, seen)
+def source_closure(source: Path) -> list[Path]:
+    """The source and every local include it reaches that exists, breadth first, each once."""
+    order: list[Path] = []
+    pending = deque([source.resolve()])
+    while pending:
+        path = pending.popleft()
+        if path in order:
+            continue
+        order.append(path)
+        text = path.read_text(encoding="utf-8", errors="ignore")
+        pending.extend(p for p in ((path.parent / inc).resolve() for inc in _LOCAL_INCLUDE.findall(text))
+                       if p.exists())
+    return order
+
+
+class KernelCache:
+    """Content-keyed hipcc builds of external kernel sources."""
+
+    def __init__(self, directory: Path | None = None):
+        self.directory = native_cache_dir(directory)
+
+    def build_command(self, compiler: str, source: Path, output: Path, flags: tuple[str, ...]) -> list[str]:
+        command = [compiler, "-O3", "-std=c++17"]
+        if Path(compiler).name.endswith("clang++"):
+            command += ["-x", "hip"]
+        if not any(flag.startswith("--offload-arch") for flag in flags):
+            command.append(f"--offload-arch={DEFAULT_OFFLOAD_ARCH}")
+        return command + [str(source), "-o", str(output), *flags]
+
+    def key(self, kernel: ResolvedNativeKernel, compiler: str) -> str:
+        digest = hashlib.sha256()
+        for path in source_closure(kernel.source_path):
+            digest.update(f"{path}\0".encode() + path.read_bytes() + b"\0")
+        for part in (kernel.benchmark, kernel.name, compiler, *kernel.compile_args):
+            digest.update(part.encode() + b"\0")
+        return digest.hexdigest()[:16]
+
+    def executable(self, kernel: ResolvedNativeKernel) -> Path:
+        compiler = _find_hip_compiler(kernel.compiler)
+        self.directory.mkdir(parents=True, exist_ok=True)
+        target = self.directory / f"{kernel.name}-{self.key(kernel, compiler)}"
+        if target.exists():
+            return target
+        staging = target.with_name(f".{target.name}.{os.getpid()}.tmp")
+        proc = subprocess.run(self.build_command(compiler, kernel.source_path, staging, kernel.compile_args),
+                              check=False, capture_output=True, text=True)
+        if proc.returncode != 0 or not staging.exists():
+            detail = proc.stderr.strip() or proc.stdout.strip() or "unknown compiler failure"
+            raise NativeKernelError(f"Failed to compile native kernel {kernel.name}: {detail}")
+        staging.chmod(0o755)
+        staging.replace(target)
+        return target
+
+    def clear(self) -> int:
+        if not self.directory.exists():
+            return 0
+        entries = list(self.directory.iterdir())
+        for entry in entries:
+            shutil.rmtree(entry) if entry.is_dir() else entry.unlink()
+        return len(entries)
+
+
+def clear_native_cache(explicit: Path | None = None) -> tuple[Path, int]:
+    cache = KernelCache(explicit)
+    return cache.directory, cache.clear()
 
 
 def prepare_native_kernel_binary(kernel: ResolvedNativeKernel) -> Path:
-    """Executable for an abi="executable" kernel: the given binary, or a cached hipcc build."""
+    """The executable of an abi="executable" kernel: its binary, or a cached build of its source."""
     if kernel.binary_path is not None:
         if not kernel.binary_path.exists():
             raise NativeKernelError(f"Native kernel binary does not exist: {kernel.binary_path}")
@@ -206,70 +252,18 @@ def prepare_native_kernel_binary(kernel: ResolvedNativeKernel) -> Path:
         raise NativeKernelError(f"Native kernel {kernel.name} is missing both source_path and binary_path.")
     if not kernel.source_path.exists():
         raise NativeKernelError(f"Native kernel source does not exist: {kernel.source_path}")
-
-    compiler = _find_hip_compiler(kernel.compiler)
-    cache = native_cache_dir(kernel.cache_dir)
-    cache.mkdir(parents=True, exist_ok=True)
-    digest = hashlib.sha256()
-    _hash_sources(digest, kernel.source_path, set())
-    for part in (kernel.benchmark, kernel.name, compiler, *kernel.compile_args):
-        digest.update(part.encode())
-    binary = cache / f"{kernel.name}-{digest.hexdigest()[:16]}"
-    if binary.exists():
-        return binary
-
-    command = [compiler, "-O3", "-std=c++17"]
-    if Path(compiler).name.endswith("clang++"):
-        command += ["-x", "hip"]
-    command += [str(kernel.source_path), "-o", str(binary), *kernel.compile_args]
-    proc = subprocess.run(command, check=False, capture_output=True, text=True)
-    if proc.returncode != 0:
-        detail = proc.stderr.strip() or proc.stdout.strip() or "unknown compiler failure"
-        raise NativeKernelError(f"Failed to compile native kernel {kernel.name}: {detail}")
-    binary.chmod(0o755)
-    return binary
+    return KernelCache(kernel.cache_dir).executable(kernel)
 
 
-def parse_native_result(stdout: str) -> NativeKernelResult:
-    lines = [line.strip() for line in stdout.splitlines() if line.strip()]
-    if not lines:
-        raise NativeKernelError("Native kernel produced no JSON output.")
+def run_native_kernel(kernel: ResolvedNativeKernel, args: list[str],
+                      timeout_s: float | None = None) -> NativeKernelResult:
+    executable = prepare_native_kernel_binary(kernel)
     try:
-        payload = json.loads(lines[-1])
-    except json.JSONDecodeError as exc:
-        raise NativeKernelError(f"Native kernel output was not valid JSON: {exc}") from exc
-    if not isinstance(payload, dict):
-        raise NativeKernelError("Native kernel output JSON must be an object.")
-    raw = payload.get("raw_metrics", {})
-    meta = payload.get("metadata", {})
-    if not isinstance(raw, dict):
-        raise NativeKernelError("Native kernel raw_metrics must be a JSON object.")
-    if not isinstance(meta, dict):
-        raise NativeKernelError("Native kernel metadata must be a JSON object.")
-    error = payload.get("error")
-    return NativeKernelResult(
-        status=str(payload.get("status", "ok")),
-        raw_metrics=dict(raw),
-        metadata=dict(meta),
-        error=None if error is None else str(error),
-    )
-
-
-def run_native_kernel(kernel: ResolvedNativeKernel, args: list[str], timeout_s: float | None = None) -> NativeKernelResult:
-    binary = prepare_native_kernel_binary(kernel)
-    env = {**os.environ, **kernel.env}
-    try:
-        proc = subprocess.run(
-            [str(binary), *args, *kernel.run_args],
-            check=False,
-            capture_output=True,
-            text=True,
-            env=env,
-            timeout=timeout_s,
-        )
+        proc = subprocess.run([str(executable), *args, *kernel.run_args], check=False, capture_output=True,
+                              text=True, env={**os.environ, **kernel.env}, timeout=timeout_s)
     except subprocess.TimeoutExpired as exc:
         raise NativeKernelError(f"Native kernel {kernel.name} timed out after {timeout_s} s") from exc
     if proc.returncode != 0:
         detail = proc.stderr.strip() or proc.stdout.strip() or "native kernel process failed"
         raise NativeKernelError(f"Native kernel {kernel.name} failed (exit status {proc.returncode}): {detail}")
-    return parse_native_result(proc.stdout)
+    return NativeKernelResult.from_stdout(proc.stdout)

@@ -1,13 +1,26 @@
-"""Profiled suite runs (behaviour of src/teamredbench/profiling/runtime.py:16-184).
+"""Profiled suite runs.
 
-The suite is re-executed as a child ``python -m teamredbench_amd run ...``
-under the engine's profiler with ``TEAMREDBENCH_INTERNAL_RUN=1`` (so the
-child does not recurse) and ``TEAMREDBENCH_FORCE_JSON_OUTPUT=1`` (so its
-records can be reloaded). The parent reloads the child's records, then runs
-the engine's extra counter passes (each writing results into its own
-directory under the artifact dir), parses the artifacts with the engine's
-``collect`` hook, and injects ``run.profiling`` -- including the parsed
-counter summary -- into the child's metadata sidecar.
+A suite with ``profiling: {engine: <name>, params: {...}}`` is measured by
+running the whole suite again in a child process under the engine's
+profiler (the behaviour of src/teamredbench/profiling/runtime.py:93-184;
+the two environment variables below are its names). :class:`ProfiledRun`
+does it in steps:
+
+  1. ``launch``   -- the engine wraps the child command
+                     (``python -m teamredbench_amd run <suite> ...``); the
+                     child gets ``TEAMREDBENCH_INTERNAL_RUN=1`` (so it does
+                     not profile itself again), ``TEAMREDBENCH_FORCE_JSON_OUTPUT=1``
+                     (so its records can be reloaded) and a run token;
+  2. ``reload``   -- the child's sidecar is the one in the output directory
+                     that carries that token (``run.run_token``), so runs
+                     sharing a directory never pick up each other's files;
+                     its JSON records become this run's records;
+  3. ``passes``   -- further runs the engine asks for: the same child under
+                     other counter groups (their records are discarded) and
+                     standalone commands (a calibration workload);
+  4. ``annotate`` -- the engine's ``collect`` hook parses the artifacts, and
+                     ``run.profiling`` (engine, commands, artifacts and the
+                     parsed counters) is written into the child's sidecar.
 """
 from __future__ import annotations
 
@@ -17,14 +30,17 @@ import os
 from pathlib import Path
 import subprocess
 import sys
+import uuid
 from typing import Any
 
-from teamredbench_amd.benchmarks.base import BenchmarkContext, BenchmarkRecord
+from teamredbench_amd.benchmarks.base import BenchmarkContext
 from teamredbench_amd.config import ProfilingConfig, SuiteConfig
-from teamredbench_amd.profiling.registry import get_profile_engine
+from teamredbench_amd.io import read_results
+from teamredbench_amd.profiling.registry import ProfilingLaunch, get_profile_engine
 
 INTERNAL_RUN_ENV = "TEAMREDBENCH_INTERNAL_RUN"
 FORCE_JSON_OUTPUT_ENV = "TEAMREDBENCH_FORCE_JSON_OUTPUT"
+RUN_TOKEN_ENV = "TEAMREDBENCH_RUN_TOKEN"
 
 
 class ProfilingError(RuntimeError):
@@ -32,44 +48,23 @@ class ProfilingError(RuntimeError):
 
 
 def profiling_active() -> bool:
+    """True inside the child run of a profiled suite."""
     return os.environ.get(INTERNAL_RUN_ENV) == "1"
 
 
 def profiling_enabled(config: ProfilingConfig) -> bool:
-    return bool(config.enabled and config.engine and not profiling_active())
-
-
-def force_json_output_enabled() -> bool:
-    return os.environ.get(FORCE_JSON_OUTPUT_ENV) == "1"
+    return bool(config.enabled and config.engine) and not profiling_active()
 
 
 def effective_output_formats(formats: list[str]) -> list[str]:
-    resolved = list(formats)
-    if force_json_output_enabled() and "json" not in resolved:
-        resolved.append("json")
-    return resolved
+    """The suite's formats, plus json when the parent of a profiled run needs to reload the records."""
+    forced = os.environ.get(FORCE_JSON_OUTPUT_ENV) == "1"
+    return list(formats) + (["json"] if forced and "json" not in formats else [])
 
 
-def _artifact_dir(output_dir: Path, suite_name: str, engine_name: str) -> Path:
-    stamp = datetime.now(timezone.utc).strftime("%Y%m%dT%H%M%SZ")
-    return output_dir / "profiling" / f"{suite_name}-{engine_name}-{stamp}"
-
-
-def _metadata_files(output_dir: Path, suite_name: str) -> set[Path]:
-    return set(output_dir.glob(f"{suite_name}-*.metadata.json")) if output_dir.exists() else set()
-
-
-def _record_from_dict(payload: dict[str, Any]) -> BenchmarkRecord:
-    return BenchmarkRecord(
-        benchmark=str(payload["benchmark"]),
-        case=str(payload["case"]),
-        dtype=str(payload["dtype"]),
-        status=str(payload.get("status", "ok")),
-        error=None if payload.get("error") is None else str(payload["error"]),
-        metrics=dict(payload.get("metrics", {})),
-        raw_metrics=dict(payload.get("raw_metrics", {})),
-        metadata=dict(payload.get("metadata", {})),
-    )
+def run_token() -> str | None:
+    """The token a profiled run's parent gave this process (recorded in the sidecar)."""
+    return os.environ.get(RUN_TOKEN_ENV)
 
 
 def child_command(suite_path: Path, device_id: int, output_dir: Path) -> list[str]:
@@ -77,67 +72,111 @@ def child_command(suite_path: Path, device_id: int, output_dir: Path) -> list[st
             "--output-dir", str(output_dir), "--quiet-records"]
 
 
-def _run(command: list[str], env: dict[str, str], what: str) -> None:
-    proc = subprocess.run(command, check=False, capture_output=True, text=True, env=env)
-    if proc.returncode != 0:
+class ProfiledRun:
+    def __init__(self, suite: SuiteConfig, output_dir: Path, device_id: int):
+        if suite.path is None:
+            raise ProfilingError("Suite path is required for profiled runs.")
+        if not suite.profiling.engine:
+            raise ProfilingError("Profiling is enabled but no engine is configured.")
+        self.suite, self.output_dir, self.device_id = suite, Path(output_dir), device_id
+        self.engine = get_profile_engine(suite.profiling.engine)
+        stamp = datetime.now(timezone.utc).strftime("%Y%m%dT%H%M%SZ")
+        self.artifact_dir = self.output_dir / "profiling" / f"{suite.name}-{self.engine.name}-{stamp}"
+        self.token = uuid.uuid4().hex
+        self.env = {**os.environ, INTERNAL_RUN_ENV: "1", FORCE_JSON_OUTPUT_ENV: "1", RUN_TOKEN_ENV: self.token}
+        self.launch_spec: ProfilingLaunch | None = None
+        self.teardown_crashes: list[dict[str, Any]] = []
+
+    # A profiler can crash in its own teardown (SIGSEGV) after the program it ran
+    # has finished and its results are written; such an exit is recorded, not
+    # fatal, when the step's output is there (`produced` says whether it is).
+    PROFILER_TEARDOWN_CRASH = (-11, 139)
+
+    def _run(self, command: list[str], what: str, produced=None) -> None:
+        proc = subprocess.run(command, capture_output=True, text=True, env=self.env, check=False)
+        if proc.returncode == 0:
+            return
+        if proc.returncode in self.PROFILER_TEARDOWN_CRASH and produced is not None and produced():
+            self.teardown_crashes.append({"step": what, "exit_status": proc.returncode})
+            return
         detail = proc.stderr.strip() or proc.stdout.strip() or "unknown profiling failure"
-        raise ProfilingError(f"{what} failed: {detail}")
+        raise ProfilingError(f"{what} failed (exit status {proc.returncode}): {detail}")
+
+    def _has_sidecar(self) -> bool:
+        try:
+            self.sidecar_path()
+        except ProfilingError:
+            return False
+        return True
+
+    def launch(self) -> None:
+        self.launch_spec = self.engine.build_command(
+            dict(self.suite.profiling.params), child_command(self.suite.path, self.device_id, self.output_dir),
+            self.artifact_dir, self.suite.path.parent)
+        self.env.update(self.launch_spec.env)
+        self._run(list(self.launch_spec.command), f"Profile engine {self.engine.name}", produced=self._has_sidecar)
+
+    def sidecar_path(self) -> Path:
+        for path in sorted(self.output_dir.glob(f"{self.suite.name}-*.metadata.json"), reverse=True):
+            try:
+                sidecar = json.loads(path.read_text(encoding="utf-8"))
+            except (OSError, json.JSONDecodeError):
+                continue
+            if sidecar.get("run", {}).get("run_token") == self.token:
+                return path
+        raise ProfilingError("Profiled run completed but no metadata file was produced.")
+
+    def passes(self) -> None:
+        spec = self.launch_spec
+        for number, prefix in enumerate(spec.extra_passes, start=1):
+            out = self.artifact_dir / f"pass{number}-results"
+            self._run([*prefix, *child_command(self.suite.path, self.device_id, out)],
+                      f"{self.engine.name} pass {number}",
+                      produced=lambda out=out: any(out.glob(f"{self.suite.name}-*.metadata.json")))
+        for number, command in enumerate(spec.standalone_passes, start=1):
+            self._run(list(command), f"{self.engine.name} standalone pass {number}",
+                      produced=lambda: any(self.artifact_dir.rglob("*counter_collection.csv")))
+
+    def profiling_metadata(self) -> dict[str, Any]:
+        spec = self.launch_spec
+        block: dict[str, Any] = {
+            "enabled": True,
+            "engine": self.engine.name,
+            "artifact_dir": str(spec.artifact_dir),
+            "command": list(spec.command),
+            "extra_passes": [list(p) for p in spec.extra_passes],
+            "standalone_passes": [list(p) for p in spec.standalone_passes],
+            "engine_metadata": dict(spec.metadata),
+        }
+        if self.teardown_crashes:
+            block["profiler_teardown_crashes"] = list(self.teardown_crashes)
+        if spec.collect is not None:
+            try:
+                block["counters"] = spec.collect(spec.artifact_dir)
+            except Exception as exc:  # noqa: BLE001 -- a parse failure must not lose the measurements
+                block["counters_error"] = f"{type(exc).__name__}: {exc}"
+        return block
 
 
 def run_profiled_suite(*, suite: SuiteConfig, context: BenchmarkContext, output_dir: Path, device_id: int,
                        record_callback):
     from teamredbench_amd.runner import RunSummary
 
-    if suite.path is None:
-        raise ProfilingError("Suite path is required for profiled runs.")
-    if not suite.profiling.engine:
-        raise ProfilingError("Profiling is enabled but no engine is configured.")
-    engine = get_profile_engine(suite.profiling.engine)
-    artifact_dir = _artifact_dir(output_dir, suite.name, engine.name)
-    launch = engine.build_command(dict(suite.profiling.params), child_command(suite.path, device_id, output_dir),
-                                  artifact_dir, suite.path.parent)
-    env = {**os.environ, INTERNAL_RUN_ENV: "1", FORCE_JSON_OUTPUT_ENV: "1", **launch.env}
-
-    before = _metadata_files(output_dir, suite.name)
-    _run(list(launch.command), env, f"Profile engine {engine.name}")
-    created = sorted(_metadata_files(output_dir, suite.name) - before)
-    if not created:
-        raise ProfilingError("Profiled run completed but no metadata file was produced.")
-    metadata_path = created[-1]
-    payload = json.loads(metadata_path.read_text(encoding="utf-8"))
-    json_path = payload.get("outputs", {}).get("json")
-    if json_path is None or not Path(json_path).exists():
-        raise ProfilingError("Profiled run did not produce a JSON results file.")
-    records = [_record_from_dict(item) for item in json.loads(Path(json_path).read_text(encoding="utf-8"))]
-
-    for index, prefix in enumerate(launch.extra_passes):
-        pass_out = artifact_dir / f"pass{index + 1}-results"
-        _run([*prefix, *child_command(suite.path, device_id, pass_out)], env, f"{engine.name} pass {index + 1}")
-    for index, command in enumerate(launch.standalone_passes):
-        _run(list(command), env, f"{engine.name} standalone pass {index + 1}")
-
-    profiling: dict[str, Any] = {
-        "enabled": True,
-        "engine": engine.name,
-        "artifact_dir": str(launch.artifact_dir),
-        "command": list(launch.command),
-        "extra_passes": [list(p) for p in launch.extra_passes],
-        "standalone_passes": [list(p) for p in launch.standalone_passes],
-        "engine_metadata": dict(launch.metadata),
-    }
-    if launch.collect is not None:
-        try:
-            profiling["counters"] = launch.collect(launch.artifact_dir)
-        except Exception as exc:  # noqa: BLE001 -- a parse failure must not lose the records
-            profiling["counters_error"] = f"{type(exc).__name__}: {exc}"
-    payload.setdefault("outputs", {})["profiling"] = str(launch.artifact_dir)
-    payload.setdefault("run", {})["profiling"] = profiling
-    metadata_path.write_text(json.dumps(payload, indent=2), encoding="utf-8")
-
-    outputs = {name: Path(p) for name, p in payload.get("outputs", {}).items()}
-    run_metadata = dict(payload.get("run", {}))
+    run = ProfiledRun(suite, output_dir, device_id)
+    run.launch()
+    sidecar_path = run.sidecar_path()
+    try:
+        sidecar, records = read_results(sidecar_path)
+    except FileNotFoundError as exc:
+        raise ProfilingError("Profiled run did not produce a JSON results file.") from exc
+    run.passes()
+    sidecar.setdefault("outputs", {})["profiling"] = str(run.launch_spec.artifact_dir)
+    sidecar.setdefault("run", {})["profiling"] = run.profiling_metadata()
+    sidecar_path.write_text(json.dumps(sidecar, indent=2), encoding="utf-8")
     if record_callback is not None:
         for record in records:
             record_callback(record)
-    return RunSummary(suite=suite, context=context, records=records, outputs=outputs, run_metadata=run_metadata,
-                      profile_note=run_metadata.get("configs", {}).get("profile_note"))
+    run_metadata = dict(sidecar["run"])
+    return RunSummary(suite=suite, context=context, records=records,
+                      outputs={name: Path(p) for name, p in sidecar["outputs"].items()},
+                      run_metadata=run_metadata, profile_note=run_metadata.get("configs", {}).get("profile_note"))

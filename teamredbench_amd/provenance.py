@@ -54,8 +54,11 @@ def build_run_metadata(
             "version": getattr(torch, "__version__", "unknown"),
             "hip_version": getattr(getattr(torch, "version", None), "hip", None),
         }
+    from teamredbench_amd.profiling.runtime import run_token
+
     hw = context.hardware_profile
     return {
+        "run_token": run_token(),
         "started_at_utc": started_at.isoformat().replace("+00:00", "Z"),
         "finished_at_utc": finished_at.isoformat().replace("+00:00", "Z"),
         "duration_s": (finished_at - started_at).total_seconds(),

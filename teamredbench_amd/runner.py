@@ -1,23 +1,28 @@
-"""Suite execution (src/teamredbench/runner.py:31-179).
+"""Running a suite: load it, set up the device context, run every benchmark
+invocation, derive metrics, write the result files.
 
-``run_suite`` loads the suite, imports its plugins, builds the context
-(device from ``LOCAL_RANK`` or ``device_id``; a hardware profile without peak
-data is replaced by the packaged profile whose SKU token -- ``mi355x`` etc. --
-matches the detected device name), runs every invocation with a record sink
-that derives metrics for ``ok`` records, and writes JSON / CSV / metadata.
-If the suite enables profiling, the run is re-executed under the profiler
-(teamredbench_amd.profiling.runtime).
+``run_suite``, ``build_context`` and ``RunSummary`` keep the reference's
+signatures (src/teamredbench/runner.py:21-179); :class:`SuiteRun` holds the
+steps. Two behaviours carried over:
+  * the device index is ``LOCAL_RANK`` when that is set, else ``device_id``;
+  * a hardware profile with no peak data (hbm bandwidth and at least one
+    compute peak) is replaced by a profile whose SKU token (``mi355x`` ...)
+    matches the detected device name, found by :class:`ProfileCatalog` in
+    the suite tree's ``configs/profiles/hardware`` or among this package's
+    profiles; the replacement is reported in ``profile_note``.
+Metrics are derived only for ``ok`` records; a skipped or failed record keeps
+its raw metrics and error and gets none.
 """
 from __future__ import annotations
 
-from dataclasses import dataclass
+from dataclasses import dataclass, field
 from datetime import datetime, timezone
 import os
 from pathlib import Path
 import re
-from typing import Callable
+from typing import Callable, Iterable
 
-from teamredbench_amd import builtin as _builtin  # noqa: F401
+from teamredbench_amd import builtin as _builtin  # noqa: F401  (registers the built-in benchmarks and metrics)
 from teamredbench_amd.benchmarks.base import BenchmarkContext, BenchmarkRecord
 from teamredbench_amd.config import HardwareProfile, SuiteConfig, load_hardware_profile, load_suite
 from teamredbench_amd.device import detect_device, load_torch
@@ -26,6 +31,52 @@ from teamredbench_amd.io import write_results
 from teamredbench_amd.profiling.runtime import effective_output_formats, profiling_enabled, run_profiled_suite
 from teamredbench_amd.provenance import build_run_metadata
 from teamredbench_amd.registry import get_benchmark, get_metric, load_plugins
+
+PACKAGED_HARDWARE_DIR = Path(__file__).resolve().parent / "configs" / "profiles" / "hardware"
+_SKU_PATTERN = re.compile(r"mi\d{3,4}x", re.IGNORECASE)
+
+
+def sku_tokens(text: str | None) -> set[str]:
+    """Instinct SKU names in a device or profile name ("AMD Instinct MI355X" -> {"mi355x"})."""
+    return {token.lower() for token in _SKU_PATTERN.findall(text or "")}
+
+
+def has_peak_data(profile: HardwareProfile) -> bool:
+    hbm = profile.peak_hbm_bandwidth_gbps
+    return bool(hbm and hbm > 0) and any(v is not None and v > 0 for v in profile.peak_compute_tops.values())
+
+
+@dataclass
+class ProfileCatalog:
+    """Hardware profiles that can stand in for one without peak data."""
+
+    directories: list[Path] = field(default_factory=list)
+
+    @classmethod
+    def packaged(cls) -> "ProfileCatalog":
+        return cls([PACKAGED_HARDWARE_DIR])
+
+    @classmethod
+    def for_suite(cls, repo_root: Path | None) -> "ProfileCatalog":
+        dirs = [repo_root / "configs" / "profiles" / "hardware"] if repo_root is not None else []
+        return cls(dirs + [PACKAGED_HARDWARE_DIR])
+
+    def candidates(self) -> Iterable[tuple[Path, HardwareProfile]]:
+        seen: set[Path] = set()
+        for directory in self.directories:
+            for path in sorted(directory.glob("*.yaml")) if directory.is_dir() else []:
+                if path.resolve() not in seen:
+                    seen.add(path.resolve())
+                    yield path, load_hardware_profile(path)
+
+    def match(self, device_name: str | None) -> HardwareProfile | None:
+        wanted = sku_tokens(device_name)
+        if not wanted:
+            return None
+        for path, profile in self.candidates():
+            if sku_tokens(f"{profile.name} {path.stem}") & wanted and has_peak_data(profile):
+                return profile
+        return None
 
 
 @dataclass
@@ -38,104 +89,87 @@ class RunSummary:
     profile_note: str | None = None
 
 
-def _apply_metrics(record: BenchmarkRecord, metric_names: list[str]) -> None:
-    if record.status != "ok":
-        return
-    for name in metric_names:
-        record.metrics[name] = get_metric(name).compute(record.raw_metrics)
-
-
-_SKU = re.compile(r"mi\d{3,4}x", re.IGNORECASE)
-
-
-def _sku_tokens(text: str | None) -> set[str]:
-    return {t.lower() for t in _SKU.findall(text or "")}
-
-
-def _has_peaks(profile: HardwareProfile) -> bool:
-    hbm = profile.peak_hbm_bandwidth_gbps
-    compute = any(v is not None and float(v) > 0 for v in profile.peak_compute_tops.values())
-    return hbm is not None and float(hbm) > 0 and compute
-
-
-def _resolve_hardware_profile(profile: HardwareProfile, *, device_name: str | None,
-                              repo_root: Path | None) -> tuple[HardwareProfile, str | None]:
-    if _has_peaks(profile) or repo_root is None:
-        return profile, None
-    wanted = _sku_tokens(device_name)
-    hardware_dir = repo_root / "configs" / "profiles" / "hardware"
-    if not wanted or not hardware_dir.exists():
-        return profile, None
-    for path in sorted(hardware_dir.glob("*.yaml")):
-        candidate = load_hardware_profile(path)
-        if _sku_tokens(f"{candidate.name} {path.stem}") & wanted and _has_peaks(candidate):
-            note = (f"Auto-selected hardware profile {candidate.name} from detected device {device_name!r} "
-                    f"because {profile.name} has no theoretical peak data.")
-            return candidate, note
-    return profile, None
+def _suite_repo_root(suite: SuiteConfig) -> Path | None:
+    # <root>/configs/suites/<suite>.yaml, the layout both trees use
+    return suite.path.parent.parent.parent if suite.path else None
 
 
 def build_context(suite: SuiteConfig, device_id: int = 0) -> tuple[BenchmarkContext, str | None]:
-    resolved_id = int(os.environ.get("LOCAL_RANK", device_id))
+    index = int(os.environ.get("LOCAL_RANK", device_id))
     torch_module = load_torch()
-    device_info = detect_device(torch_module, device_id=resolved_id)
-    repo_root = suite.path.parent.parent.parent if suite.path else None
-    profile, note = _resolve_hardware_profile(
-        suite.hardware_profile, device_name=device_info.name if device_info else None, repo_root=repo_root
-    )
+    device = detect_device(torch_module, device_id=index)
+    profile, note = suite.hardware_profile, None
+    if not has_peak_data(profile) and device is not None:
+        stand_in = ProfileCatalog.for_suite(_suite_repo_root(suite)).match(device.name)
+        if stand_in is not None:
+            note = (f"Auto-selected hardware profile {stand_in.name} from detected device {device.name!r} "
+                    f"because {profile.name} has no theoretical peak data.")
+            profile = stand_in
     context = BenchmarkContext(
         hardware_profile=profile,
         runtime_profile=suite.runtime_profile,
-        device_info=device_info,
+        device_info=device,
         torch_module=torch_module,
         dtype_specs=discover_dtypes(torch_module),
-        device_id=resolved_id,
-        repo_root=repo_root,
+        device_id=index,
+        repo_root=_suite_repo_root(suite),
         suite_path=suite.path,
     )
     return context, note
 
 
-def run_suite(
-    suite_path: str | Path,
-    output_dir: str | Path | None = None,
-    device_id: int = 0,
-    record_callback: Callable[[BenchmarkRecord], None] | None = None,
-) -> RunSummary:
-    started = datetime.now(timezone.utc)
-    suite = load_suite(suite_path)
-    load_plugins(suite.plugins)
-    target = Path(output_dir).resolve() if output_dir else suite.outputs.directory
-    context, note = build_context(suite, device_id=device_id)
-    suite.hardware_profile = context.hardware_profile
-    if profiling_enabled(suite.profiling):
-        return run_profiled_suite(suite=suite, context=context, output_dir=target.resolve(), device_id=device_id,
-                                  record_callback=record_callback)
+class SuiteRun:
+    """One execution of a suite file."""
 
-    records: list[BenchmarkRecord] = []
-    for invocation in suite.benchmarks:
-        cls = get_benchmark(invocation.benchmark)
-        metric_names = invocation.metrics or list(cls.default_metrics)
+    def __init__(self, suite_path: str | Path, output_dir: str | Path | None, device_id: int,
+                 record_callback: Callable[[BenchmarkRecord], None] | None):
+        self.started = datetime.now(timezone.utc)
+        self.suite = load_suite(suite_path)
+        load_plugins(self.suite.plugins)
+        self.output_dir = (Path(output_dir) if output_dir else self.suite.outputs.directory).resolve()
+        self.device_id = device_id
+        self.record_callback = record_callback
+        self.context, self.profile_note = build_context(self.suite, device_id=device_id)
+        self.suite.hardware_profile = self.context.hardware_profile
+        self.records: list[BenchmarkRecord] = []
 
-        def sink(record: BenchmarkRecord, metric_names: list[str] = metric_names) -> None:
-            _apply_metrics(record, metric_names)
-            if record_callback is not None:
-                record_callback(record)
+    def _sink_for(self, metric_names: list[str]) -> Callable[[BenchmarkRecord], None]:
+        metrics = [get_metric(name) for name in metric_names]
 
-        records.extend(cls(context=context, params=invocation.params, record_sink=sink).run())
+        def sink(record: BenchmarkRecord) -> None:
+            if record.ok:
+                for metric in metrics:
+                    record.metrics[metric.name] = metric.compute(record.raw_metrics)
+            if self.record_callback is not None:
+                self.record_callback(record)
 
-    formats = effective_output_formats(suite.outputs.formats)
-    run_metadata = build_run_metadata(
-        suite=suite,
-        context=context,
-        requested_device_id=device_id,
-        output_dir=target.resolve(),
-        output_formats=formats,
-        profile_note=note,
-        started_at=started,
-        finished_at=datetime.now(timezone.utc),
-    )
-    outputs = write_results(records=records, suite_name=suite.name, output_dir=target.resolve(), formats=formats,
-                            run_metadata=run_metadata)
-    return RunSummary(suite=suite, context=context, records=records, outputs=outputs, run_metadata=run_metadata,
-                      profile_note=note)
+        return sink
+
+    def execute(self) -> None:
+        for invocation in self.suite.benchmarks:
+            cls = get_benchmark(invocation.benchmark)
+            sink = self._sink_for(invocation.metrics or list(cls.default_metrics))
+            self.records.extend(cls(context=self.context, params=invocation.params, record_sink=sink).run())
+
+    def finish(self) -> RunSummary:
+        formats = effective_output_formats(self.suite.outputs.formats)
+        run_metadata = build_run_metadata(
+            suite=self.suite, context=self.context, requested_device_id=self.device_id,
+            output_dir=self.output_dir, output_formats=formats, profile_note=self.profile_note,
+            started_at=self.started, finished_at=datetime.now(timezone.utc),
+        )
+        outputs = write_results(records=self.records, suite_name=self.suite.name, output_dir=self.output_dir,
+                                formats=formats, run_metadata=run_metadata)
+        return RunSummary(suite=self.suite, context=self.context, records=self.records, outputs=outputs,
+                          run_metadata=run_metadata, profile_note=self.profile_note)
+
+
+def run_suite(suite_path: str | Path, output_dir: str | Path | None = None, device_id: int = 0,
+              record_callback: Callable[[BenchmarkRecord], None] | None = None) -> RunSummary:
+    run = SuiteRun(suite_path, output_dir, device_id, record_callback)
+    if profiling_enabled(run.suite.profiling):
+        # the whole suite runs again in a child process under the profiler
+        return run_profiled_suite(suite=run.suite, context=run.context, output_dir=run.output_dir,
+                                  device_id=device_id, record_callback=record_callback)
+    run.execute()
+    return run.finish()

@@ -1,7 +1,9 @@
-"""Torch-backend helpers (src/teamredbench/utils.py:14-48) plus seeded inputs.
+"""Input generation and the torch backend's timing.
 
-``timed_iterations`` is the reference's wall-clock mean between device
-synchronisations. The native backend times with hipEvents inside the
+``timed_iterations`` is the torch backend's clock (the semantics of
+src/teamredbench/utils.py:14-29): run the op `warmup` times, synchronise the
+device, then report the wall-clock mean of `iterations` calls bracketed by
+device synchronisations. The native backend times with hipEvents inside the
 library instead (mb_time_stream / mb_time_gemm).
 """
 from __future__ import annotations
@@ -19,31 +21,34 @@ def synchronize(torch_module: Any) -> None:
 
 
 def timed_iterations(fn: Callable[[], None], *, torch_module: Any, warmup: int, iterations: int) -> float:
-    for _ in range(warmup):
+    """Mean seconds per call of `fn`, after `warmup` untimed calls."""
+    calls = max(iterations, 1)
+    for _ in range(max(warmup, 0)):
         fn()
     synchronize(torch_module)
-    start = time.perf_counter()
-    for _ in range(iterations):
+    began = time.perf_counter()
+    for _ in range(calls):
         fn()
     synchronize(torch_module)
-    return (time.perf_counter() - start) / max(iterations, 1)
+    return (time.perf_counter() - began) / calls
+
+
+def _random_of_kind(torch: Any, kind: str, shape: tuple[int, ...], device: Any, dtype: Any):
+    """Unseeded random values for one dtype kind, in a type torch can draw them in."""
+    if kind == "bool":
+        return torch.randint(0, 2, shape, device=device, dtype=torch.uint8)
+    if kind == "integer":
+        return torch.randint(0, 17, shape, device=device, dtype=dtype)
+    if kind == "complex":
+        part = torch.float32 if dtype == torch.complex64 else torch.float64
+        return torch.complex(torch.randn(shape, device=device, dtype=part), torch.randn(shape, device=device, dtype=part))
+    return torch.randn(shape, device=device, dtype=torch.float32)
 
 
 def make_tensor(torch_module: Any, spec: DTypeSpec, shape: tuple[int, ...], device: Any):
-    """Unseeded random tensor of `spec` (the reference torch backend's inputs)."""
-    torch = torch_module
-    dtype = getattr(torch, spec.torch_attr)
-    if spec.kind == "bool":
-        return torch.randint(0, 2, shape, device=device, dtype=torch.uint8).to(dtype=dtype)
-    if spec.kind == "integer":
-        return torch.randint(0, 17, shape, device=device, dtype=dtype)
-    if spec.kind == "complex":
-        real_dtype = torch.float32 if spec.name == "complex64" else torch.float64
-        return torch.complex(
-            torch.randn(shape, device=device, dtype=real_dtype),
-            torch.randn(shape, device=device, dtype=real_dtype),
-        ).to(dtype=dtype)
-    return torch.randn(shape, device=device, dtype=torch.float32).to(dtype=dtype)
+    """An unseeded random tensor of `spec` (for dtypes the seeded generators below do not cover)."""
+    dtype = getattr(torch_module, spec.torch_attr)
+    return _random_of_kind(torch_module, spec.kind, shape, device, dtype).to(dtype=dtype)
 
 
 def seeded_uniform(torch_module: Any, numel: int, dtype_name: str, device: Any, seed: int):

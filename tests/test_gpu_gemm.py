@@ -45,6 +45,11 @@ def tiled_impl(dtype: str, k: int, info: dict) -> str:
         return "gfx950_mfma16_lds_dma"
     return "gfx950_mfma32_lds_dma"
 
+def splitk_workspace(info: dict, m: int, n: int) -> int:
+    """Workspace a split plan needs: the fp32 partial planes, [splits][M][N]."""
+    return info["split_k"] * m * n * 4 if info["split_k"] > 1 else 0
+
+
 def _gemm(lib, dtype: str, a: torch.Tensor, b: torch.Tensor, sa: float = 1.0, sb: float = 1.0) -> torch.Tensor:
     m, k = a.shape
     n = b.shape[1]
@@ -142,8 +147,8 @@ def test_n_multiple_of_128_takes_128x128_tiles(lib, dtype, shape, tune):
 @pytest.mark.parametrize("shape, tile_m", [((2048, 2048, 2048), 128), ((1024, 1024, 1024), 64), ((640, 1536, 768), 64)])
 def test_few_tiles_take_128x128_tiles(lib, dtype, shape, tile_m):
     # Several tile rows that would leave half the CUs idle on 128 x 256 tiles
-    # run 128 x 128 tiles, unsplit (the default plan, not an override); when
-    # twice their block count still fits in half the CUs, 64 x 128 tiles.
+    # run 128 x 128 tiles, unsplit (the default plan, not an override); the
+    # smallest of them 64 x 128 tiles, which the cost model rates faster there.
     m, n, k = shape
     info = lib.gemm_info(capi.DTYPES[dtype], m, n, k)
     assert (info["tile_m"], info["tile_n"], info["split_k"]) == (tile_m, 128, 1)
@@ -152,25 +157,26 @@ def test_few_tiles_take_128x128_tiles(lib, dtype, shape, tile_m):
 
 
 @pytest.mark.parametrize("dtype, shape, tile_m", [("bfloat16", (16, 8192, 8192), 64), ("float16", (16, 8192, 8192), 64),
-                                                  ("bfloat16", (128, 8192, 8192), 64),
+                                                  ("bfloat16", (128, 8192, 8192), 128),
                                                   ("float16", (128, 8192, 8192), 128)])
-def test_skinny_benchmark_shapes_split_two_ways_on_128x128_tiles(lib, dtype, shape, tile_m):
-    # The split-K cost model's pick for the two skinny benchmark shapes with 16-bit inputs: 2 splits over
-    # 128 x 128 tiles (measured 24.7 / 31.4 us against 25.9 / 32.2 for 4 splits over 128 x 256 tiles, and
-    # 31 / 45 us for the 16 / 8 splits a tile-count rule picks); 64 x 128 tiles then take the same
-    # split count when the blocks fit in half the CUs, or (bf16 and fp8) for one 128-row tile in all.
+def test_skinny_benchmark_shapes_split_four_ways(lib, dtype, shape, tile_m):
+    # The split cost model's pick for the two skinny benchmark shapes with 16-bit inputs: 4 splits, one
+    # block per CU (with B streamed from HBM, 16 x 8192 x 8192 bf16 ran 29.2 us against 35.5 for 2
+    # splits and 32.8 for 8; 128 x 8192 x 8192 38.5 us against 48.6 and 45.3).
     m, n, k = shape
     info = lib.gemm_info(capi.DTYPES[dtype], m, n, k)
-    assert (info["tile_m"], info["tile_n"], info["split_k"]) == (tile_m, 128, 2)
-    assert lib.gemm_workspace_size(capi.DTYPES[dtype], m, n, k) == 2 * m * n * 4
+    assert (info["tile_m"], info["tile_n"], info["split_k"]) == (tile_m, 128, 4)
+    assert info["grid_blocks"] == 256
+    assert lib.gemm_workspace_size(capi.DTYPES[dtype], m, n, k) == splitk_workspace(info, m, n)
     _check_random(lib, dtype, m, n, k, seed=m, rows=64)
 
 
 @pytest.mark.parametrize("dtype", ["float8_e4m3fn", "float8_e5m2"])
 def test_fp8_skinny_takes_128x128_tiles(lib, dtype):
-    # As for 16-bit inputs: 2 splits, and 64 x 128 tiles for a problem of one 128-row tile.
+    # As for 16-bit inputs: 4 splits of 128 x 128 tiles, one block per CU (25.2 us against 28.0 for 2
+    # splits of 64 x 128 tiles, B from HBM).
     info = lib.gemm_info(capi.DTYPES[dtype], 128, 8192, 8192)
-    assert (info["tile_m"], info["tile_n"], info["split_k"]) == (64, 128, 2)
+    assert (info["tile_m"], info["tile_n"], info["split_k"]) == (128, 128, 4)
     _check_random(lib, dtype, 128, 8192, 8192, seed=5, rows=64)
 
 
@@ -178,14 +184,14 @@ def test_fp8_skinny_takes_128x128_tiles(lib, dtype):
 @pytest.mark.parametrize("shape", [(1, 4096, 4096), (16, 8192, 8192), (128, 8192, 8192), (100, 2048, 4096)])
 def test_skinny_shapes_split_k(lib, dtype, shape):
     # The skinny GEMM configurations: ragged M on the tiled kernel, K split
-    # over an fp32 workspace and summed by the reduction kernel.
+    # over an fp32 workspace and summed by the split blocks that arrive last.
     m, n, k = shape
     info = lib.gemm_info(capi.DTYPES[dtype], m, n, k)
     splits = info["split_k"]
     # M <= 4 with 16-bit inputs streams B through the small-M kernel instead
     expect = "gfx950_gemv_stream" if m <= 4 and dtype in ("bfloat16", "float16") else tiled_impl(dtype, k, info)
     assert info["implementation"] == expect and splits >= 2
-    assert info["workspace_bytes"] == splits * m * n * 4
+    assert info["workspace_bytes"] == splitk_workspace(info, m, n)
     print(f"[gemm] skinny {dtype} {shape} split {splits}", flush=True)
     _check_random(lib, dtype, m, n, k, seed=m)
 
@@ -442,7 +448,7 @@ def test_small_m_stream_kernel(lib, dtype, m, nk):
     n, k = nk
     info = lib.gemm_info(capi.DTYPES[dtype], m, n, k)
     assert info["implementation"] == "gfx950_gemv_stream"
-    assert info["workspace_bytes"] == (info["split_k"] * m * n * 4 if info["split_k"] > 1 else 0)
+    assert info["workspace_bytes"] == splitk_workspace(info, m, n)
     print(f"[gemm] small-m {dtype} m={m} n={n} k={k} splits={info['split_k']}", flush=True)
     ops = rp.gemm_inputs(m, n, k, dtype, seed=m * 7 + k)
     got = _gemm(lib, dtype, ops["a"], ops["b"]).float()
@@ -466,6 +472,46 @@ def test_small_m_one_split_writes_c_directly(lib):
     m, n, k = 2, 65544, 64
     info = lib.gemm_info(capi.DT_BFLOAT16, m, n, k)
     assert info["split_k"] == 1 and info["workspace_bytes"] == 0
+
+
+@pytest.mark.parametrize("dtype, config, splits, shape", [
+    ("bfloat16", 3, 4, (128, 2048, 4096)), ("float16", 2, 8, (100, 1024, 8192)),
+    ("float8_e4m3fn", 2, 4, (128, 1024, 8192)), ("bfloat16", 1, 2, (64, 2048, 2048)),
+    ("bfloat16", -1, 16, (1, 4096, 4096)), ("float16", -1, 32, (3, 2048, 8192)),
+])
+def test_split_handoff_over_back_to_back_launches(lib, dtype, config, splits, shape, tune):
+    # The split blocks hand their partials to the tile's last arrival through one workspace that every
+    # launch reuses: 24 launches queued back to back on one stream, alternating two operand sets, each
+    # into its own C. A partial or arrival count carried over from an earlier launch, or a stale copy of
+    # the workspace in a cache, would make some C differ from its set's first result.
+    m, n, k = shape
+    if config >= 0:
+        tune(gemm_tiled_config=config)
+    tune(gemm_splits=splits)
+    dt = capi.DTYPES[dtype]
+    info = lib.gemm_info(dt, m, n, k)
+    assert info["split_k"] == splits, info
+    print(f"[gemm] split handoff {dtype} {shape} {info['implementation']} {info['tile_m']}x{info['tile_n']} "
+          f"split {splits}", flush=True)
+    sets = [rp.gemm_inputs(m, n, k, dtype, seed=s) for s in (11, 12)]
+    dev = [(o["a"].cuda(), o["b"].cuda()) for o in sets]
+    ws_bytes = lib.gemm_workspace_size(dt, m, n, k)
+    ws = torch.full((ws_bytes,), 0xA5, dtype=torch.uint8, device="cuda")
+    stream = torch.cuda.current_stream().cuda_stream
+    outs = []
+    for i in range(24):
+        (a, b), ops = dev[i % 2], sets[i % 2]
+        c = torch.full((m, n), float("nan"), dtype=rp.gemm_output_dtype(dtype), device="cuda")
+        lib.gemm(dt, a.data_ptr(), b.data_ptr(), c.data_ptr(), m, n, k, ops["scale_a"], ops["scale_b"],
+                 ws.data_ptr(), ws_bytes, stream)
+        outs.append(c)
+    torch.cuda.synchronize()
+    for i, c in enumerate(outs):
+        assert torch.equal(c.view(torch.int16), outs[i % 2].view(torch.int16)), f"launch {i} differs from launch {i % 2}"
+    for j in range(2):
+        got = outs[j].cpu().float()
+        ref = rp.gemm_reference(sets[j]["a"], sets[j]["b"], sets[j]["scale_a"], sets[j]["scale_b"])
+        assert rp.rel_frobenius(got, ref) <= REL_FROB[dtype]
 
 
 @pytest.mark.parametrize("dtype", ["bfloat16", "float8_e4m3fn"])

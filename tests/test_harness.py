@@ -273,7 +273,9 @@ def test_prepare_native_kernel_binary_rebuilds_when_local_include_changes(tmp_pa
     assert native_runtime.prepare_native_kernel_binary(kernel) == first and len(outputs) == 1  # cached
     include.write_text("static constexpr int kValue = 1;\n", encoding="utf-8")
     second = native_runtime.prepare_native_kernel_binary(kernel)
-    assert first != second and outputs == [first, second]
+    assert first != second and len(outputs) == 2 and first.exists() and second.exists()
+    # each build lands under a temporary name first and is renamed into place
+    assert all(not out.exists() and out.name.endswith(".tmp") for out in outputs)
 
 
 def test_clean_native_cache_command_removes_entries(tmp_path: Path):
@@ -326,3 +328,79 @@ def test_generic_profile_is_replaced_by_the_detected_sku(monkeypatch):
     context, note = runner_mod.build_context(suite)
     assert context.hardware_profile.name == "amd-instinct-mi355x"
     assert note and "Auto-selected" in note
+
+
+# ---------------------------------------------------------------- record status and result files
+@register_benchmark("test_parity_outcomes")
+class ParityOutcomeBenchmark(Benchmark):
+    """Emits one record whose in-run parity check passed and one whose check failed."""
+
+    default_metrics = ["latency_us", "hbm_bandwidth_gbps"]
+
+    def run(self) -> list[BenchmarkRecord]:
+        raw = {"elapsed_s": 0.002, "moved_bytes": 2e9, "peak_bandwidth_gbps": 8000.0}
+        return [self.measured(case=case, dtype="float32", raw_metrics=dict(raw),
+                              metadata={"parity": {"vs": "torch", "max_ulp": ulp, "bound_ulp": 1, "passed": ulp <= 1}})
+                for case, ulp in (("good", 0), ("bad", 7))]
+
+
+def test_a_failed_parity_check_fails_the_record_and_the_cli(tmp_path: Path):
+    from typer.testing import CliRunner
+
+    from teamredbench_amd.cli import app
+
+    suite = _write_suite(tmp_path, "parity", [{"benchmark": "test_parity_outcomes"}], formats=("json", "csv"))
+    good, bad = run_suite(suite).records
+    assert good.status == "ok" and good.metrics["hbm_bandwidth_gbps"] == pytest.approx(1000.0)
+    # the wrong kernel keeps its timing for diagnosis but publishes no rate
+    assert bad.status == "failed" and bad.metrics == {} and bad.raw_metrics["elapsed_s"] == 0.002
+    assert "parity" in bad.error and "max_ulp=7" in bad.error
+    result = CliRunner().invoke(app, ["run", str(suite)])
+    assert result.exit_code == 1
+    assert "[FAILED] test_parity_outcomes case=bad" in result.stdout and "(1 failed)" in result.stdout
+    sidecar = json.loads(next((tmp_path / "results").glob("parity-*.metadata.json")).read_text(encoding="utf-8"))
+    assert sidecar["record_status_counts"] == {"ok": 1, "failed": 1}
+
+
+def test_record_round_trips_through_its_result_forms():
+    record = BenchmarkRecord(benchmark="mfu", case="gemm_8x8x8", dtype="bfloat16", raw_metrics={"elapsed_s": 1e-6},
+                             metadata={"parity": {"passed": True}, "shape": [8, 8, 8]}, metrics={"mfu_pct": 1.5})
+    assert BenchmarkRecord.from_dict(json.loads(json.dumps(record.to_dict()))) == record
+    row = record.to_row()
+    assert row["metric_mfu_pct"] == 1.5 and row["error"] == ""
+    assert json.loads(row["meta_parity"]) == {"passed": True} and json.loads(row["meta_shape"]) == [8, 8, 8]
+
+
+def test_unknown_output_formats_are_reported_not_fatal(tmp_path: Path):
+    suite = _write_suite(tmp_path, "formats", [{"benchmark": "test_dummy_callback"}], formats=("json", "parquet"))
+    summary = run_suite(suite)
+    sidecar = json.loads(summary.outputs["metadata"].read_text(encoding="utf-8"))
+    assert set(summary.outputs) == {"json", "metadata"} and sidecar["ignored_formats"] == ["parquet"]
+
+
+@pytest.mark.parametrize("mutate, message", [
+    (lambda doc: doc.update(benchmarks=[{"benchmark": "hbm", "params": [1, 2]}]), "benchmarks[0].params must be a mapping"),
+    (lambda doc: doc.update(benchmarks=[{"params": {}}]), "benchmarks[0].benchmark is required"),
+    (lambda doc: doc.update(device={}), "device.profile is required"),
+    (lambda doc: doc.update(plugins="not-a-list"), "plugins must be a list"),
+])
+def test_malformed_suites_name_the_offending_key(tmp_path: Path, mutate, message):
+    from teamredbench_amd.config import ConfigError
+
+    suite = _write_suite(tmp_path, "broken", [{"benchmark": "test_dummy_callback"}])
+    doc = yaml.safe_load(suite.read_text(encoding="utf-8"))
+    mutate(doc)
+    suite.write_text(yaml.safe_dump(doc), encoding="utf-8")
+    with pytest.raises(ConfigError, match=message.replace("[", r"\[").replace("]", r"\]")):
+        load_suite(suite)
+
+
+def test_discover_suggests_the_packaged_profile_of_the_detected_sku(monkeypatch):
+    from teamredbench_amd import device
+
+    monkeypatch.setattr(device, "detect_device", lambda torch_module, device_id=0: DeviceInfo(index=0, name="AMD Instinct MI355X"))
+    monkeypatch.setattr(device, "_run_command", lambda command: None)
+    payload = device.discover_environment(None)
+    assert payload["suggested_hardware_profile"]["name"] == "amd-instinct-mi355x"
+    assert payload["suggested_hardware_profile"]["peak_hbm_bandwidth_gbps"] == 8000
+    assert payload["runtime"]["hipcc_version"] is None and "cuda_api_version" not in payload["runtime"]["torch"]

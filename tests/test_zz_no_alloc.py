@@ -86,7 +86,9 @@ def test_noalloc_without_partials_matches(lib):
 
 
 def test_noalloc_rejects_shapes_beyond_the_scratch_array(lib, tune):
-    # 4096^3 forced to 2 K splits needs 2 * 4096 * 4096 * 4 = 128 MiB of partials: refused before any launch
+    # 4096^3 forced to 2 K splits (on 128 x 256 tiles: 256-row tiles never split) needs
+    # 2 * 4096 * 4096 * 4 = 128 MiB of partials: refused before any launch
+    tune(gemm_tiled_config=1)
     tune(gemm_splits=2)
     need = lib.gemm_workspace_size(capi.DT_BFLOAT16, 4096, 4096, 4096)
     assert need > capi.NOALLOC_SCRATCH_BYTES
