@@ -212,6 +212,10 @@ def main() -> int:
                         help="timed CPU iterations at the GPU step's 2^28 size, beside the 2^24 CPU triad "
                              "configuration (0 = that configuration only); --no-cpu skips the CPU baseline")
     parser.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    parser.add_argument("--calibration-copy", action="store_true",
+                        help="before the triad, launch the fp32 copy kernel 3 times over 2^28 elements (1 GiB read, "
+                             "1 GiB written per launch, untimed): the known traffic that scales FETCH_SIZE / "
+                             "WRITE_SIZE when rocprofv3 counter passes run over this command")
     args = parser.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -231,6 +235,16 @@ def main() -> int:
 
     lib = capi.load_library()  # raises if the HIP library is missing or stale: no fallback
 
+    if args.calibration_copy:
+        _log("calibration: 3 copy launches over 2^28 fp32 elements")
+        src = torch.zeros(TRIAD_ELEMENTS, device="cuda", dtype=torch.float32)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            lib.stream(capi.OP_COPY, capi.DT_FLOAT32, dst.data_ptr(), src.data_ptr(), None, TRIAD_ELEMENTS, 1.0, 0,
+                       torch.cuda.current_stream().cuda_stream)
+        torch.cuda.synchronize()
+        del src, dst
+        torch.cuda.empty_cache()
     _log(f"triad fp32 2^28: warmup {args.warmup}, steps {args.steps}")
     triad = bench_triad(torch, lib, capi, args.steps, args.warmup)
     value = triad["moved_bytes"] / triad["wall_s_per_step"] / 1e9

@@ -113,6 +113,32 @@ def build(verbose: bool = False, jobs: int | None = None) -> Path:
     return out
 
 
+EXAMPLES_DIR = PACKAGE_DIR / "native" / "examples"
+EXAMPLE_CACHE_DIR = LIB_DIR / "exec_cache"
+
+
+def example_params(source: Path) -> dict:
+    """The `hbm` suite params that select an example executable and its in-tree build cache."""
+    return {"native": {"source": str(source), "cache_dir": str(EXAMPLE_CACHE_DIR)}}
+
+
+def build_examples() -> list[Path]:
+    """Build the example external kernels (native/examples/*.hip) through the same content-keyed
+    cache a suite selecting them uses, so a suite run finds them built (and rebuilds one only if
+    its source or compiler changed). Returns the executables."""
+    import teamredbench_amd.native.builtin  # noqa: F401  (the built-in names the benchmark defaults to)
+    from teamredbench_amd.native.runtime import prepare_native_kernel_binary, resolve_native_kernel
+
+    built = []
+    for source in sorted(EXAMPLES_DIR.glob("*.hip")):
+        kernel = resolve_native_kernel(benchmark="hbm", params=example_params(source), suite_path=None,
+                                       repo_root=PACKAGE_DIR.parent, default_kernel="hbm_hip")
+        built.append(prepare_native_kernel_binary(kernel))
+    return built
+
+
 if __name__ == "__main__":
     path = build(verbose=True)
     print(path)
+    for exe in build_examples():
+        print(exe)

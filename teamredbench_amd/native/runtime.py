@@ -205,9 +205,11 @@ class KernelCache:
         return command + [str(source), "-o", str(output), *flags]
 
     def key(self, kernel: ResolvedNativeKernel, compiler: str) -> str:
+        # paths relative to the source's directory: a moved tree keeps its builds
         digest = hashlib.sha256()
+        root = kernel.source_path.resolve().parent
         for path in source_closure(kernel.source_path):
-            digest.update(f"{path}\0".encode() + path.read_bytes() + b"\0")
+            digest.update(f"{os.path.relpath(path, root)}\0".encode() + path.read_bytes() + b"\0")
         for part in (kernel.benchmark, kernel.name, compiler, *kernel.compile_args):
             digest.update(part.encode() + b"\0")
         return digest.hexdigest()[:16]

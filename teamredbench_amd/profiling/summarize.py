@@ -146,6 +146,34 @@ def mfma(directory: Path, kernel: str, durations_us: list[float], xcds: int, cus
     return "\n".join(lines)
 
 
+def sidecar(path: Path, match: str | None = None) -> str:
+    """The rocprofv3 counter summary a profiled suite run attached to its metadata sidecar
+    (run.profiling.counters), one line per kernel (those matching `match`, a regex, if given)."""
+    import json
+
+    doc = json.loads(path.read_text(encoding="utf-8"))
+    block = doc.get("run", {}).get("profiling", {})
+    counters = block.get("counters")
+    if not counters:
+        raise SystemExit(f"{path} carries no run.profiling.counters ({block.get('counters_error', 'no profiling')})")
+    lines = [f"suite: {doc.get('suite_name')}  records: {doc.get('record_count')}  engine: {block.get('engine')}",
+             f"calibration factors: {counters.get('_calibration', {})}"]
+    for name, entry in sorted(counters.items()):
+        if name.startswith("_") or (match and not re.search(match, name)):
+            continue
+        parts = [f"{entry.get('dispatches', 0):4d} x {entry.get('avg_duration_ns', 0) / 1e3:9.2f} us"]
+        if "dram_fetch_bytes" in entry and "dram_write_bytes" in entry:
+            parts.append(f"DRAM read {entry['dram_fetch_bytes']:.4g} B write {entry['dram_write_bytes']:.4g} B")
+        if "dram_gbps" in entry:
+            parts.append(f"{entry['dram_gbps']:.1f} GB/s")
+        if "mfma_busy_pct" in entry:
+            parts.append(f"MFMA busy {entry['mfma_busy_pct']:.1f}%")
+        if "clock_ghz" in entry:
+            parts.append(f"{entry['clock_ghz']:.2f} GHz")
+        lines.append(f"{'  '.join(parts)}  {_short(name, 90)}")
+    return "\n".join(lines)
+
+
 def main(argv: list[str] | None = None) -> int:
     parser = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     sub = parser.add_subparsers(dest="cmd", required=True)
@@ -169,6 +197,9 @@ def main(argv: list[str] | None = None) -> int:
     p_mfma.add_argument("--cus", type=int, default=256)
     p_suite = sub.add_parser("suite")
     p_suite.add_argument("csv", type=Path, nargs="+")
+    p_side = sub.add_parser("sidecar", help="counter summary of a profiled suite run's metadata sidecar")
+    p_side.add_argument("path", type=Path)
+    p_side.add_argument("--match", help="only kernels whose name matches this regex")
     args = parser.parse_args(argv)
     if args.cmd == "suite":
         print(suite(args.csv))
@@ -176,6 +207,8 @@ def main(argv: list[str] | None = None) -> int:
         print(mfma(args.directory, args.kernel, args.duration_us, args.xcds, args.cus))
     elif args.cmd == "stats":
         print(stats(args.directory, args.top))
+    elif args.cmd == "sidecar":
+        print(sidecar(args.path, args.match))
     else:
         print(traffic(args.fetch, args.write, args.kernel, args.calibrate, args.calibrate_read,
                       args.calibrate_write, args.algorithmic_bytes))

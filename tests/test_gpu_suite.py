@@ -102,3 +102,26 @@ def test_profiled_suite_attaches_counters(tmp_path: Path):
     assert abs(dram / algorithmic - 1) <= 0.02
     gemm = [v for k, v in counters.items() if "gemm_tiled_kernel" in k]
     assert gemm and all(0 < g["mfma_busy_pct"] <= 100 for g in gemm), gemm
+
+
+def test_external_executable_runs_through_the_registry(tmp_path: Path):
+    # A third-party kernel in the reference's executable contract: native/examples/stream_exec.hip,
+    # built by hipcc for gfx950 through the content-keyed cache (build() prebuilt it, so the suite finds
+    # it there), run once per case with the reference's argv, its last stdout line parsed as the record.
+    from teamredbench_amd.native import build
+
+    source = build.EXAMPLES_DIR / "stream_exec.hip"
+    params = {"backend": "native", "dtypes": ["float32", "bfloat16"], "modes": ["copy", "scale", "triad"],
+              "size_mib": 256, "scale": 3.0, "warmup": 2, "iterations": 10, **build.example_params(source)}
+    print("[suite] external executable example", flush=True)
+    summary = run_suite(_write_suite(tmp_path, "external", [{"benchmark": "hbm", "params": params}]))
+    f32 = [r for r in summary.records if r.dtype == "float32"]
+    assert len(f32) == 3
+    for record in f32:
+        assert record.status == "ok", record.error
+        assert record.metadata["implementation"] == "example_stream_exec"
+        assert record.metadata["arch"].startswith("gfx950")
+        assert record.metrics["hbm_bandwidth_gbps"] > 100 and record.raw_metrics["moved_bytes"] > 0
+    # the example takes float32 only: other dtypes come back as the executable's own skip
+    bf16 = [r for r in summary.records if r.dtype == "bfloat16"]
+    assert len(bf16) == 3 and all(r.status == "skipped" and "float32" in r.error for r in bf16)

@@ -404,3 +404,19 @@ def test_discover_suggests_the_packaged_profile_of_the_detected_sku(monkeypatch)
     assert payload["suggested_hardware_profile"]["name"] == "amd-instinct-mi355x"
     assert payload["suggested_hardware_profile"]["peak_hbm_bandwidth_gbps"] == 8000
     assert payload["runtime"]["hipcc_version"] is None and "cuda_api_version" not in payload["runtime"]["torch"]
+
+
+def test_example_executable_is_prebuilt_under_the_key_a_suite_resolves():
+    # build() builds native/examples/*.hip into the in-tree cache under the content key that a suite
+    # selecting the example resolves to, so the GPU box runs it without compiling.
+    import teamredbench_amd.native.builtin  # noqa: F401
+    from teamredbench_amd.native import build
+
+    source = build.EXAMPLES_DIR / "stream_exec.hip"
+    kernel = native_runtime.resolve_native_kernel(benchmark="hbm", params=build.example_params(source),
+                                                  suite_path=Path("/elsewhere/suite.yaml"), repo_root=None,
+                                                  default_kernel="hbm_hip")
+    assert kernel.abi == "executable" and kernel.source_path == source and kernel.cache_dir == build.EXAMPLE_CACHE_DIR
+    cache = native_runtime.KernelCache(kernel.cache_dir)
+    expected = cache.directory / f"{kernel.name}-{cache.key(kernel, native_runtime._find_hip_compiler())}"
+    assert expected in build.build_examples() and expected.exists()
