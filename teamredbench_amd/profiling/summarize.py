@@ -174,6 +174,60 @@ def sidecar(path: Path, match: str | None = None) -> str:
     return "\n".join(lines)
 
 
+def _by_launch_shape(pmc_dir: Path) -> tuple[dict[str, dict[str, float]], dict[str, float]]:
+    """Counters (median per dispatch) and dispatch durations, keyed by kernel name plus launch shape,
+    so the same kernel launched with other block sizes or grids stays apart."""
+    from statistics import median
+
+    per: dict[tuple[str, str], dict[str, float]] = {}
+    spans: dict[tuple[str, str], int] = {}
+    for path in sorted(pmc_dir.rglob("*counter_collection.csv")):
+        with path.open(newline="", encoding="utf-8", errors="replace") as handle:
+            for row in csv.DictReader(handle):
+                key = (f"{row.get('Kernel_Name', '?')} [{row.get('Workgroup_Size')} x "
+                       f"{int(row.get('Grid_Size') or 0) // max(int(row.get('Workgroup_Size') or 1), 1)}]",
+                       row.get("Dispatch_Id", "?"))
+                counters = per.setdefault(key, {})
+                counters[row["Counter_Name"]] = counters.get(row["Counter_Name"], 0.0) + float(row["Counter_Value"])
+                spans[key] = int(row["End_Timestamp"]) - int(row["Start_Timestamp"])
+    grouped: dict[str, dict[str, list[float]]] = {}
+    for (name, dispatch), counters in per.items():
+        entry = grouped.setdefault(name, {})
+        for counter, value in counters.items():
+            entry.setdefault(counter, []).append(value)
+        entry.setdefault("_ns", []).append(spans[(name, dispatch)])
+    values = {k: {c: median(v) for c, v in cs.items() if c != "_ns"} for k, cs in grouped.items()}
+    return values, {k: median(cs["_ns"]) for k, cs in grouped.items()}
+
+
+def traffic_mix(latency_dir: Path, stall_dir: Path, xcds: int, channels: int) -> str:
+    """Memory-side behaviour per kernel from two counter passes: (1) TCC_EA0_RDREQ_LEVEL_sum,
+    TCC_EA0_RDREQ_sum, TCC_EA0_WRREQ_LEVEL_sum, TCC_EA0_WRREQ_sum, GRBM_GUI_ACTIVE; (2)
+    TCC_EA0_RDREQ_DRAM_CREDIT_STALL_sum, TCC_EA0_WRREQ_DRAM_CREDIT_STALL_sum, GRBM_GUI_ACTIVE. Average
+    EA read / write latency = LEVEL / requests (cycles); requests in flight = LEVEL / cycles; a credit
+    stall is the fraction of channel-cycles (channels per XCD x XCDs) a request waited for DRAM credit."""
+    lat, durations = _by_launch_shape(latency_dir)
+    stall, _ = _by_launch_shape(stall_dir)
+    lines = [f"{'us':>8} {'rd req':>9} {'wr req':>9} {'rd lat':>7} {'wr lat':>7} {'rd fly':>7} {'wr fly':>7} "
+             f"{'GHz':>5} {'rdstall':>7} {'wrstall':>7}  kernel"]
+    for name in sorted(lat):
+        a, b = lat[name], stall.get(name, {})
+        if not a.get("GRBM_GUI_ACTIVE"):
+            continue
+        cycles = a["GRBM_GUI_ACTIVE"] / xcds
+        rd, wr = a.get("TCC_EA0_RDREQ_sum", 0.0), a.get("TCC_EA0_WRREQ_sum", 0.0)
+        rdl, wrl = a.get("TCC_EA0_RDREQ_LEVEL_sum", 0.0), a.get("TCC_EA0_WRREQ_LEVEL_sum", 0.0)
+        ns = durations.get(name, 0.0)
+        per_channel = cycles * xcds * channels
+        lines.append(
+            f"{ns / 1e3:8.1f} {rd:9.3g} {wr:9.3g} {rdl / rd if rd else 0:7.0f} {wrl / wr if wr else 0:7.0f} "
+            f"{rdl / cycles:7.0f} {wrl / cycles:7.0f} {cycles / ns if ns else 0:5.2f} "
+            f"{b.get('TCC_EA0_RDREQ_DRAM_CREDIT_STALL_sum', 0.0) / per_channel:7.3f} "
+            f"{b.get('TCC_EA0_WRREQ_DRAM_CREDIT_STALL_sum', 0.0) / per_channel:7.3f}  {_short(name, 60)}"
+            f"{name[name.rindex(' ['):] if ' [' in name else ''}")
+    return "\n".join(lines)
+
+
 def main(argv: list[str] | None = None) -> int:
     parser = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     sub = parser.add_subparsers(dest="cmd", required=True)
@@ -197,6 +251,11 @@ def main(argv: list[str] | None = None) -> int:
     p_mfma.add_argument("--cus", type=int, default=256)
     p_suite = sub.add_parser("suite")
     p_suite.add_argument("csv", type=Path, nargs="+")
+    p_mix = sub.add_parser("mix", help="EA read / write latency, requests in flight and DRAM credit stalls")
+    p_mix.add_argument("latency_dir", type=Path)
+    p_mix.add_argument("stall_dir", type=Path)
+    p_mix.add_argument("--xcds", type=int, default=8)
+    p_mix.add_argument("--channels", type=int, default=16, help="TCC channels per XCD")
     p_side = sub.add_parser("sidecar", help="counter summary of a profiled suite run's metadata sidecar")
     p_side.add_argument("path", type=Path)
     p_side.add_argument("--match", help="only kernels whose name matches this regex")
@@ -207,6 +266,8 @@ def main(argv: list[str] | None = None) -> int:
         print(mfma(args.directory, args.kernel, args.duration_us, args.xcds, args.cus))
     elif args.cmd == "stats":
         print(stats(args.directory, args.top))
+    elif args.cmd == "mix":
+        print(traffic_mix(args.latency_dir, args.stall_dir, args.xcds, args.channels))
     elif args.cmd == "sidecar":
         print(sidecar(args.path, args.match))
     else:
