@@ -35,7 +35,9 @@
 // evenly between the MFMAs. The barrier is a bare s_barrier preceded by an
 // explicit vmcnt wait for the loads of stage k + 1 only, derived at compile
 // time from the issue order (load_schedule) -- a full __syncthreads() would
-// wait for all of them.
+// wait for all of them. Each step's first two MFMAs go out ahead of its
+// barrier, from operands already in registers, so the MFMA pipe stays busy
+// while the wave waits there.
 //
 // Waves form a WGM x WGN grid; each wave owns (BM/WGM) x (BN/WGN) of C as
 // 32 x 32 fragments: v_mfma_f32_32x32x16_{bf16,f16} (two per stage), or for
@@ -61,6 +63,15 @@ namespace mb {
 namespace {
 
 constexpr int kStageK = 64;                  // bytes of K per row per stage
+// MFMAs of a step issued ahead of its barrier. They take operands already in
+// registers, and the MFMA pipe works through them while the wave waits at the
+// barrier (one wave per SIMD: nothing else would keep it busy). Two measured
+// best: against one, fp8 8192^3 +1.0%, 8192 x 1024 x 8192 +1.9%, 16-bit
+// shapes +0.3-0.5%; three and four lose on 128-row tiles.
+#ifndef MB_PRE_BARRIER_MFMA
+#define MB_PRE_BARRIER_MFMA 2
+#endif
+constexpr int kPreBarrierMfma = MB_PRE_BARRIER_MFMA;
 
 __device__ __forceinline__ int swz_b16(int k) { return ((k << 2) ^ (k << 1)) & 15; }
 // fp8 B rows of 256 bytes (256 columns) and of 128 bytes (128 columns).
@@ -497,7 +508,9 @@ gemm_tiled_kernel(const unsigned char* __restrict__ A, const unsigned char* __re
         constexpr int A_LOADS = ODD ? A_INSTR : 0;
         constexpr int LOADS = A_LOADS + B_INSTR;
         constexpr int N_MEM = N_READS + LOADS;              // memory instructions this step
-        constexpr int PER = (N_MEM + N_MFMA - 1) / N_MFMA;  // ... issued after each MFMA
+        constexpr int PRE = N_MFMA >= 16 ? kPreBarrierMfma : 0;   // MFMAs before the barrier (long steps)
+        static_assert(PRE >= 0 && PRE < N_MFMA, "pre-barrier MFMAs must leave slots for the memory instructions");
+        constexpr int PER = (N_MEM + N_MFMA - PRE - 1) / (N_MFMA - PRE);  // ... issued after each later MFMA
         // Memory instruction m is a load when m + 1 is one of the first LOADS
         // multiples of kStride, otherwise the next operand read: the loads
         // sit evenly among the reads (A pair loads first, then B).
@@ -509,14 +522,18 @@ gemm_tiled_kernel(const unsigned char* __restrict__ A, const unsigned char* __re
         unsigned char* load_b = b_slot(std::integral_constant<int, I % NB>{});
         const StageOps& cur = ops[I % 2];
         StageOps& nxt = ops[(I + 1) % 2];
-        wait_vmcnt_and_barrier<ODD ? kSched.odd_wait : kSched.even_wait>();
         const int bload = min(kt + NB, last);
         const int aload = min((kt - 1) / 2 + NA, last_pair);
         [&]<int... Q>(std::integer_sequence<int, Q...>) {
             ([&] {
+                if constexpr (Q == PRE) {
+                    wait_vmcnt_and_barrier<ODD ? kSched.odd_wait : kSched.even_wait>();
+                    __builtin_amdgcn_sched_barrier(0);   // the scheduler would hoist the next MFMA above it
+                }
                 mfma_op(std::integral_constant<int, Q>{}, cur);
-                constexpr int lo = Q * PER < N_MEM ? Q * PER : N_MEM;
-                constexpr int hi = Q * PER + PER < N_MEM ? Q * PER + PER : N_MEM;
+                constexpr int S = Q < PRE ? 0 : (Q - PRE) * PER;
+                constexpr int lo = Q < PRE ? 0 : S < N_MEM ? S : N_MEM;
+                constexpr int hi = Q < PRE ? 0 : S + PER < N_MEM ? S + PER : N_MEM;
                 [&]<int... R>(std::integer_sequence<int, R...>) {
                     ([&] {
                         constexpr int m = lo + R;
@@ -840,14 +857,14 @@ gemm_fp8_mi16_kernel(const unsigned char* __restrict__ A, const unsigned char* _
         constexpr int LOADS = A_LOADS + B_INSTR;
         constexpr int N_MFMA = HALF_ROWS * FN;
         constexpr int N_OTHER = LOADS + 2 * FN;   // loads first, then this stage's next-pair B reads
-        constexpr int PER = (N_OTHER + N_MFMA - 1) / N_MFMA;
+        constexpr int PRE = kPreBarrierMfma < FN ? kPreBarrierMfma : FN - 1;   // MFMAs before the barrier,
+        static_assert(PRE >= 0, "within the step's first fragment row");
+        constexpr int PER = (N_OTHER + N_MFMA - PRE - 1) / (N_MFMA - PRE);
         const unsigned char* a_cur = a_slot(std::integral_constant<int, (I / 2) % NA>{});
         const unsigned char* a_next = a_slot(std::integral_constant<int, (I / 2 + 1) % NA>{});
         const unsigned char* b_read = b_slot(std::integral_constant<int, (I + 2) % NB>{});
         unsigned char* a_load = a_slot(std::integral_constant<int, (I / 2 + NA - 1) % NA>{});
         unsigned char* b_load = b_slot(std::integral_constant<int, (I + 1) % NB>{});
-        wait_vmcnt_and_barrier<H ? kSched.odd_wait : kSched.even_wait>();
-        launder_offsets();
         const int aload = min((kt >> 1) + NA - 1, last_pair);
         const int bload = min(kt + 1 + NB, last);
         // Other memory instruction m is a load when m + 1 is one of the first
@@ -858,14 +875,22 @@ gemm_fp8_mi16_kernel(const unsigned char* __restrict__ A, const unsigned char* _
             ([&] {
                 constexpr int i = H * HALF_ROWS + Q / FN, j = Q % FN;
                 constexpr int row_pos = (I / 2) * FM + i;   // position in the unrolled loop
+                if constexpr (Q == PRE) {
+                    wait_vmcnt_and_barrier<H ? kSched.odd_wait : kSched.even_wait>();
+                    __builtin_amdgcn_sched_barrier(0);   // the scheduler would hoist the next MFMA above it
+                    launder_offsets();
+                }
                 acc[i][j] = mfma16_fp8<DT>(bop[CUR][j], aop[row_pos % (A_AHEAD + 1)], acc[i][j]);
-                if constexpr (j == 0) {
+                // The next fragment row's A read follows the row's first MFMA, or for the step's first
+                // row the barrier (a read before it would hold the barrier's LDS wait).
+                if constexpr (Q / FN == 0 ? Q == PRE : j == 0) {
                     constexpr int ahead = (row_pos + A_AHEAD) % (A_AHEAD + 1);
                     if constexpr (i + A_AHEAD < FM) read_a(a_cur, i + A_AHEAD, aop[ahead]);
                     else read_a(a_next, i + A_AHEAD - FM, aop[ahead]);
                 }
-                constexpr int lo = Q * PER < N_OTHER ? Q * PER : N_OTHER;
-                constexpr int hi = Q * PER + PER < N_OTHER ? Q * PER + PER : N_OTHER;
+                constexpr int S = Q < PRE ? 0 : (Q - PRE) * PER;
+                constexpr int lo = Q < PRE ? 0 : S < N_OTHER ? S : N_OTHER;
+                constexpr int hi = Q < PRE ? 0 : S + PER < N_OTHER ? S + PER : N_OTHER;
                 [&]<int... R>(std::integer_sequence<int, R...>) {
                     ([&] {
                         constexpr int m = lo + R;
