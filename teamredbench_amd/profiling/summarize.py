@@ -17,6 +17,13 @@
         units were busy, and the clock it ran at over the dispatch duration
         (the counter run's own timestamps unless --duration-us is given).
 
+    python -m teamredbench_amd.profiling.summarize waits <dir> --kernel <regex>
+        each SQ_WAIT* / SQ_ACTIVE_INST* / SQ_INST_CYCLES* / SQ_LDS* counter of
+        a counter run as a share of SQ_WAVE_CYCLES (the wave-cycles the
+        kernel's waves existed), per matching kernel: SQ_WAIT_ANY is time in
+        s_waitcnt and barriers, SQ_WAIT_INST_ANY time with an instruction that
+        could not issue yet.
+
     python -m teamredbench_amd.profiling.summarize suite <results.csv> [...]
         one line per record of a suite run's CSV output: for GEMM records the
         shape, dtype, kernel configuration (tile, K splits), latency, TFLOP/s,
@@ -146,6 +153,22 @@ def mfma(directory: Path, kernel: str, durations_us: list[float], xcds: int, cus
     return "\n".join(lines)
 
 
+def waits(directory: Path, kernel: str) -> str:
+    rx = re.compile(kernel)
+    counters = {k: v for k, v in parse_counters(directory).items() if rx.search(k)}
+    if not counters:
+        raise SystemExit(f"no kernel matching {kernel!r} under {directory}")
+    shares = ("SQ_WAIT", "SQ_ACTIVE_INST", "SQ_INST_CYCLES", "SQ_LDS", "SQ_BUSY_CYCLES")
+    lines = []
+    for name, values in sorted(counters.items()):
+        lines.append(f"kernel: {_short(name)}")
+        wave = values.get("SQ_WAVE_CYCLES")
+        for key in sorted(values):
+            share = f"  ({100.0 * values[key] / wave:.1f}% of SQ_WAVE_CYCLES)" if wave and key.startswith(shares) else ""
+            lines.append(f"  {key}: {values[key]:.6g}{share}")
+    return "\n".join(lines)
+
+
 def sidecar(path: Path, match: str | None = None) -> str:
     """The rocprofv3 counter summary a profiled suite run attached to its metadata sidecar
     (run.profiling.counters), one line per kernel (those matching `match`, a regex, if given)."""
@@ -249,6 +272,9 @@ def main(argv: list[str] | None = None) -> int:
                         help="average duration of each matching kernel, in name order")
     p_mfma.add_argument("--xcds", type=int, default=8)
     p_mfma.add_argument("--cus", type=int, default=256)
+    p_waits = sub.add_parser("waits", help="SQ wait and issue counters as shares of SQ_WAVE_CYCLES")
+    p_waits.add_argument("directory", type=Path)
+    p_waits.add_argument("--kernel", required=True)
     p_suite = sub.add_parser("suite")
     p_suite.add_argument("csv", type=Path, nargs="+")
     p_mix = sub.add_parser("mix", help="EA read / write latency, requests in flight and DRAM credit stalls")
@@ -264,6 +290,8 @@ def main(argv: list[str] | None = None) -> int:
         print(suite(args.csv))
     elif args.cmd == "mfma":
         print(mfma(args.directory, args.kernel, args.duration_us, args.xcds, args.cus))
+    elif args.cmd == "waits":
+        print(waits(args.directory, args.kernel))
     elif args.cmd == "stats":
         print(stats(args.directory, args.top))
     elif args.cmd == "mix":

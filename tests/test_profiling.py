@@ -211,3 +211,22 @@ def test_suite_summary_formats_gemm_records(tmp_path: Path):
     assert len(gemm) == 3
     assert gemm[1].split() == ["gemm_16x8192x8192", "bfloat16", "128x256", "4", "26.25", "81.8", "3.3", "5133"]
     assert gemm[2].split() == ["gemm_2048x2048x2048", "bfloat16", "128x128", "1", "21.30", "806.5", "32.3", "-"]
+
+
+def test_waits_summary_shares_of_wave_cycles(tmp_path: Path):
+    # `summarize waits` divides each SQ wait / issue counter by SQ_WAVE_CYCLES of the same kernel; other
+    # counters are printed without a share, and kernels not matching --kernel are left out.
+    from teamredbench_amd.profiling import summarize
+
+    rows = (_counter_rows(GEMM, "SQ_WAVE_CYCLES", 2.0e8, 3) + _counter_rows(GEMM, "SQ_WAIT_ANY", 2.5e7, 3)
+            + _counter_rows(GEMM, "SQ_WAIT_INST_LDS", 1.0e7, 3) + _counter_rows(GEMM, "GRBM_GUI_ACTIVE", 5.0e6, 3)
+            + _counter_rows(TRIAD, "SQ_WAVE_CYCLES", 1.0e6, 2, first_id=10))
+    _write_csv(tmp_path / "sq" / "host" / "1" / "run_counter_collection.csv", rows)
+    lines = summarize.waits(tmp_path / "sq", "gemm_").splitlines()
+    assert lines[0].startswith("kernel: ") and "gemm_tiled_kernel" in lines[0] and len(lines) == 5
+    by_name = {line.split(":")[0].strip(): line for line in lines[1:]}
+    assert by_name["SQ_WAIT_ANY"].endswith("(12.5% of SQ_WAVE_CYCLES)")
+    assert by_name["SQ_WAIT_INST_LDS"].endswith("(5.0% of SQ_WAVE_CYCLES)")
+    assert "%" not in by_name["GRBM_GUI_ACTIVE"]
+    with pytest.raises(SystemExit):
+        summarize.waits(tmp_path / "sq", "no_such_kernel")
