@@ -10,7 +10,8 @@
 // chunk), several chunks in flight. The 8 partial sums of a column are added
 // through LDS at the end. K is split over blocks until the
 // grid covers the GPU twice; the splits' fp32 partials go to the caller's
-// workspace and a second kernel adds them and rounds once.
+// workspace and a second kernel adds them (gemm_gemv_reduce_kernel) and
+// rounds once.
 #include "gemm_common.hpp"
 
 #include <algorithm>
@@ -115,25 +116,40 @@ gemm_gemv_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B,
     }
 }
 
-// C[i] = round(sum_s ws[s][i]) over `splits` partial planes of mn elements
-// (mn % 4 == 0), 4 elements per thread, 8 planes' loads in flight at a time.
+// C[i] = round(sum_s ws[s][i]) over `splits` partial planes of mn elements.
+// A block takes 64 consecutive elements; its wave w adds planes w, w + 4, ...
+// with up to 16 loads in flight at once, so up to 64 splits cost one trip to
+// memory (the planes were just written by the previous kernel: the pass is
+// latency-bound), and the four waves' sums meet in LDS and are added in wave
+// order.
+constexpr int kGvReduceCols = 64;
+constexpr int kGvReduceWaves = 4;
+constexpr int kGvReduceLoads = 16;   // planes per wave in flight
+
 template <int DT>
-__global__ void __launch_bounds__(256)
+__global__ void __launch_bounds__(kGvReduceCols * kGvReduceWaves)
 gemm_gemv_reduce_kernel(const float* __restrict__ ws, uint16_t* __restrict__ C, int64_t mn, int splits) {
-    const int64_t q = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (4 * q >= mn) return;
-    f32x4 s = {0.f, 0.f, 0.f, 0.f};
-    for (int p0 = 0; p0 < splits; p0 += 8) {
-        f32x4 v[8];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int64_t i = (int64_t)blockIdx.x * kGvReduceCols + lane;
+    float s = 0.f;
+    for (int p0 = 0; p0 < splits; p0 += kGvReduceWaves * kGvReduceLoads) {
+        float v[kGvReduceLoads];
 #pragma unroll
-        for (int j = 0; j < 8; ++j)
-            v[j] = p0 + j < splits ? *reinterpret_cast<const f32x4*>(ws + (int64_t)(p0 + j) * mn + 4 * q)
-                                   : (f32x4){0.f, 0.f, 0.f, 0.f};
+        for (int j = 0; j < kGvReduceLoads; ++j) {
+            const int p = p0 + wave + kGvReduceWaves * j;
+            v[j] = (p < splits && i < mn) ? ws[(int64_t)p * mn + i] : 0.f;
+        }
 #pragma unroll
-        for (int j = 0; j < 8; ++j) s += v[j];
+        for (int j = 0; j < kGvReduceLoads; ++j) s += v[j];
     }
-    const uint16_t r0 = round16<DT>(s[0]), r1 = round16<DT>(s[1]), r2 = round16<DT>(s[2]), r3 = round16<DT>(s[3]);
-    *reinterpret_cast<u32x2*>(C + 4 * q) = (u32x2){(unsigned)r0 | ((unsigned)r1 << 16), (unsigned)r2 | ((unsigned)r3 << 16)};
+    __shared__ float red[kGvReduceWaves][kGvReduceCols];
+    red[wave][lane] = s;
+    __syncthreads();
+    if (wave != 0 || i >= mn) return;
+    float t = red[0][lane];
+#pragma unroll
+    for (int w = 1; w < kGvReduceWaves; ++w) t += red[w][lane];
+    C[i] = round16<DT>(t);
 }
 
 template <int DT, int MR>
@@ -148,9 +164,10 @@ int launch_m(const void* A, const void* B, void* C, int64_t M, int64_t N, int64_
                        (int)N, (int)K, k_len, ws);
     MB_HIP_TRY(hipGetLastError());
     if (splits > 1) {
-        const int64_t mn = M * N;   // N % 8 == 0, so mn % 4 == 0
-        hipLaunchKernelGGL(gemm_gemv_reduce_kernel<DT>, dim3((unsigned)((mn / 4 + 255) / 256)), dim3(256), 0, stream,
-                           static_cast<const float*>(ws), static_cast<uint16_t*>(C), mn, splits);
+        const int64_t mn = M * N;
+        hipLaunchKernelGGL(gemm_gemv_reduce_kernel<DT>, dim3((unsigned)((mn + kGvReduceCols - 1) / kGvReduceCols)),
+                           dim3(kGvReduceCols * kGvReduceWaves), 0, stream, static_cast<const float*>(ws),
+                           static_cast<uint16_t*>(C), mn, splits);
         MB_HIP_TRY(hipGetLastError());
     }
     return MB_OK;

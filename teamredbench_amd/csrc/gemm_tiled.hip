@@ -963,24 +963,28 @@ gemm_fp8_mi16_kernel(const unsigned char* __restrict__ A, const unsigned char* _
 }
 
 // Sum of the K-split partials: C[m][n] = alpha * sum_s ws[s][m][n], rounded
-// once to the output type. Each thread handles 4 consecutive columns.
-template <int DT>
+// once to the output type. Each thread handles 4 consecutive columns and has
+// L splits' loads in flight at once, L the split count rounded up to a power
+// of two (at most 32): the planes were just written by the GEMM kernel, so
+// the pass is latency-bound. The adds keep split order.
+template <int DT, int L>
 __global__ void __launch_bounds__(256)
 gemm_splitk_reduce_kernel(const float* __restrict__ ws, unsigned char* __restrict__ C, int64_t quads,
                           int64_t plane, int splits, float alpha) {
+    constexpr int kLoads = L;
     const int64_t q = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (q >= quads) return;
-    f32x4 sum = *reinterpret_cast<const f32x4*>(ws + 4 * q);
-    // Four splits' loads in flight at a time; the adds keep split order.
-    int s = 1;
-    for (; s + 3 < splits; s += 4) {
-        f32x4 v[4];
+    f32x4 sum = {-0.f, -0.f, -0.f, -0.f};   // -0 + x == x for every x, so the sum starts exactly at split 0
+    for (int s0 = 0; s0 < splits; s0 += kLoads) {
+        f32x4 v[kLoads];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) v[u] = *reinterpret_cast<const f32x4*>(ws + (s + u) * plane + 4 * q);
+        for (int u = 0; u < kLoads; ++u)
+            v[u] = s0 + u < splits ? *reinterpret_cast<const f32x4*>(ws + (s0 + u) * plane + 4 * q)
+                                   : f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int u = 0; u < 4; ++u) sum += v[u];
+        for (int u = 0; u < kLoads; ++u)
+            if (s0 + u < splits) sum += v[u];
     }
-    for (; s < splits; ++s) sum += *reinterpret_cast<const f32x4*>(ws + s * plane + 4 * q);
     *reinterpret_cast<u32x2*>(C + 8 * q) = pack4<DT>(sum[0] * alpha, sum[1] * alpha, sum[2] * alpha, sum[3] * alpha);
 }
 
@@ -1024,9 +1028,11 @@ int launch_cfg(const void* A, const void* B, void* C, int64_t M, int64_t N, int6
     MB_HIP_TRY(hipGetLastError());
     if (splits > 1) {
         const int64_t quads = M * N / 4;
-        hipLaunchKernelGGL(gemm_splitk_reduce_kernel<DT>, dim3((unsigned)((quads + 255) / 256)), dim3(256), 0,
-                           stream, static_cast<const float*>(ws), static_cast<unsigned char*>(C), quads, M * N,
-                           splits, alpha);
+        auto reduce = splits <= 4 ? gemm_splitk_reduce_kernel<DT, 4>
+                    : splits <= 8 ? gemm_splitk_reduce_kernel<DT, 8>
+                    : splits <= 16 ? gemm_splitk_reduce_kernel<DT, 16> : gemm_splitk_reduce_kernel<DT, 32>;
+        hipLaunchKernelGGL(reduce, dim3((unsigned)((quads + 255) / 256)), dim3(256), 0, stream,
+                           static_cast<const float*>(ws), static_cast<unsigned char*>(C), quads, M * N, splits, alpha);
         MB_HIP_TRY(hipGetLastError());
     }
     return MB_OK;
