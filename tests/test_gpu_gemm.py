@@ -118,9 +118,10 @@ def test_tiled_stage_counts(lib, dtype, config, ksteps, tune):
 
 
 @pytest.mark.parametrize("dtype", ["bfloat16", "float8_e4m3fn"])
-@pytest.mark.parametrize("splits, ksteps", [(3, 15), (3, 21), (5, 35), (7, 7)])
+@pytest.mark.parametrize("splits, ksteps", [(3, 15), (3, 21), (5, 35), (7, 7), (40, 80), (64, 128)])
 def test_forced_splits_with_odd_stage_counts(lib, dtype, splits, ksteps, tune):
-    # Each split runs ksteps / splits stages (odd here), writing fp32 partials.
+    # Each split runs ksteps / splits stages (odd for the first four), writing fp32 partials; 40 and 64 splits take the
+    # reduction past one round of 32 in-flight loads (a partial second round, a full one).
     tune(gemm_splits=splits)
     k = ksteps * (64 if dtype.startswith("float8") else 32)
     m, n = 128, 512
@@ -441,10 +442,12 @@ def test_f32_lds_dma_constant_fill_is_exact(lib):
 
 @pytest.mark.parametrize("dtype", ["bfloat16", "float16"])
 @pytest.mark.parametrize("m", [1, 2, 3, 4])
-@pytest.mark.parametrize("nk", [(4096, 4096), (8, 8), (24, 1000), (1032, 72), (8192, 8192), (65544, 64)])
+@pytest.mark.parametrize("nk", [(4096, 4096), (8, 8), (24, 1000), (1032, 72), (8192, 8192), (65544, 64),
+                                (256, 65536), (8, 131072)])
 def test_small_m_stream_kernel(lib, dtype, m, nk):
     # M <= 4 streams B with fp32 FMAs; every element within the output rounding plus an fp32
-    # accumulation bound of an fp64 brute force. 65544 x 64 keeps one K split (C written directly).
+    # accumulation bound of an fp64 brute force. 65544 x 64 keeps one K split (C written directly);
+    # 256 x 65536 and 8 x 131072 split K 512 ways, so the reduction adds its planes over 8 rounds.
     n, k = nk
     info = lib.gemm_info(capi.DTYPES[dtype], m, n, k)
     assert info["implementation"] == "gfx950_gemv_stream"
