@@ -270,7 +270,11 @@ __device__ __forceinline__ u32x2 pack4(float a, float b, float c, float d) {
 // row by row and stored so that 16 (8) lanes write one 256-byte (128-byte) C
 // row segment: whole cache lines. Read-backs go out in batches of BATCH
 // before their stores, so no store waits on the LDS read just before it.
-// Rows at or past M (a partial last tile) are not stored.
+// The stores are nontemporal: nothing in the kernel reads C back, and every
+// CU stores its tile at about the same moment, so keeping those lines out of
+// L2 lets the burst drain faster (measured +0.6% at 8192^3, +1.8% at 4096^3,
+// +2.6% at fp8 8192 x 1024 x 8192). Rows at or past M (a partial last tile)
+// are not stored.
 template <int WTM, int ROW_BYTES>
 __device__ __forceinline__ void store_staged_tile(const unsigned char* stage, unsigned char* C, int M, int N,
                                                   int row_base, int64_t col_base, int lane) {
@@ -294,7 +298,7 @@ __device__ __forceinline__ void store_staged_tile(const unsigned char* stage, un
         }
 #pragma unroll
         for (int p = 0; p < BATCH; ++p) {
-            if (grow < M) *reinterpret_cast<u32x4*>(cptr) = rows[p];
+            if (grow < M) __builtin_nontemporal_store(rows[p], reinterpret_cast<u32x4*>(cptr));
             grow += ROWS_PER_STORE;
             cptr += ROWS_PER_STORE * ldc;
         }
