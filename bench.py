@@ -13,7 +13,11 @@ in HBM. The printed JSON line carries:
                        `traffic` is the HBM bytes per launch from the committed
                        rocprofv3 FETCH_SIZE/WRITE_SIZE summary, when present;
   gemm                 bf16 and fp8 e4m3 GEMM TFLOPS and MFU at 8192^3
-                       (event-timed, same library), with a sampled parity check;
+                       (event-timed, same library), with a sampled parity check,
+                       and each one's CPU baseline: torch.mm on CPU tensors over
+                       a 512-row slab of the same problem (bf16 operands for
+                       bf16; for fp8, whose torch.mm has no CPU kernel, the
+                       dequantised fp32 operands the oracle multiplies);
   cpu_baseline         the reference torch op (torch.add(b, c, alpha=3.0,
                        out=a)) on CPU tensors on this host's cores: the CPU
                        triad configuration (2^24 elements, seed 0, 5 warmup +
@@ -201,6 +205,42 @@ def cpu_baseline(large_iterations: int) -> dict:
     return out
 
 
+GEMM_CPU_ROWS = 512
+
+
+def cpu_gemm_baseline(dtype: str, size: int, rows: int = GEMM_CPU_ROWS, min_seconds: float = 2.0) -> dict:
+    """torch.mm on CPU tensors (the reference torch path, mfu.py:229-238) over a rows x size slab of A
+    against the whole size x size B: 1 untimed call, then timed calls until min_seconds have passed (at
+    most 5). bf16 multiplies bf16 tensors; fp8 e4m3 multiplies fp32 tensors, the dequantised values the
+    oracle uses, since torch.mm has no CPU kernel for float8. Threads: every CPU this process may use."""
+    import torch
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    gen = torch.Generator().manual_seed(0)
+    a = torch.randn(rows, size, generator=gen) / math.sqrt(size)
+    b = torch.randn(size, size, generator=gen) / math.sqrt(size)
+    if dtype == "bfloat16":
+        a, b = a.to(torch.bfloat16), b.to(torch.bfloat16)
+    c = torch.empty(rows, size, dtype=a.dtype)
+    torch.mm(a, b, out=c)
+    calls, t0 = 0, time.perf_counter()
+    while calls < 1 or (time.perf_counter() - t0 < min_seconds and calls < 5):
+        torch.mm(a, b, out=c)
+        calls += 1
+    per = (time.perf_counter() - t0) / calls
+    operands = "bf16" if dtype == "bfloat16" else "fp32 (dequantised fp8)"
+    return {
+        "value": 2.0 * rows * size * size / per / 1e12,
+        "unit": "TFLOP/s",
+        "cores": cores,
+        "kind": "port",
+        "sample": (f"torch.mm on {operands} CPU tensors, a {rows} x {size} slab of A against the {size} x {size} B "
+                   f"({2.0 * rows * size * size / 1e9:.1f} GFLOP per call), 1 untimed + {calls} timed calls, "
+                   f"{per * 1e3:.1f} ms per call"),
+    }
+
+
 def main() -> int:
     parser = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     parser.add_argument("--gpus", type=int, default=1)
@@ -264,6 +304,10 @@ def main() -> int:
         _log("cpu baseline: 2^24 fp32 triad, 5 warmup + 20 timed")
         baseline = cpu_baseline(args.cpu_iterations)
         _log(f"cpu baseline: {baseline['value']:.1f} GB/s on {baseline['cores']} threads")
+        for dtype, entry in gemm.items():
+            _log(f"cpu baseline: torch.mm {dtype}, {GEMM_CPU_ROWS} x 8192 x 8192 slab")
+            entry["cpu_baseline"] = cpu_gemm_baseline(dtype, 8192)
+            _log(f"cpu baseline: {entry['cpu_baseline']['value']:.3f} TFLOPS ({entry['cpu_baseline']['sample']})")
 
     traffic = read_traffic()
     line = {
