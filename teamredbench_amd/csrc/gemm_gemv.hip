@@ -25,6 +25,7 @@ constexpr int kGvHalfWaves = 8;      // 4 waves x 2 half-waves, each on its own 
 constexpr int kGvChunk = 8;          // consecutive K rows per half-wave chunk (one 16-byte A load)
 constexpr int kGvUnroll = 2;         // chunks in flight per lane
 constexpr int kGvMaxM = 4;
+constexpr int64_t kGvMaxSplits = 512;   // the reduction adds up to 512 planes in one trip
 
 typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 
@@ -117,39 +118,59 @@ gemm_gemv_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B,
 }
 
 // C[i] = round(sum_s ws[s][i]) over `splits` partial planes of mn elements.
-// A block takes 64 consecutive elements; its wave w adds planes w, w + 4, ...
-// with up to 16 loads in flight at once, so up to 64 splits cost one trip to
-// memory (the planes were just written by the previous kernel: the pass is
-// latency-bound), and the four waves' sums meet in LDS and are added in wave
-// order.
+// A block of W waves takes 64 consecutive elements; its wave w adds planes
+// w, w + W, ... with L loads in flight at once, so W * L splits cost one trip
+// to memory (the planes were just written by the previous kernel: the pass is
+// latency-bound), and the waves' sums meet in LDS and are added in wave order.
+// Above 16 splits the launch takes 16 waves, each with the fewest loads that
+// cover the split count in one trip: a wave with fewer loads in flight is
+// done sooner, and on MI355X 16 waves of 8 loads added 128 splits of a
+// 1 x 1024 partial 0.7 us sooner than 4 waves of 32 (7.9 vs 8.6 us for the
+// whole 1 x 1024 x 8192 product).
 constexpr int kGvReduceCols = 64;
-constexpr int kGvReduceWaves = 4;
-constexpr int kGvReduceLoads = 16;   // planes per wave in flight
 
-template <int DT>
-__global__ void __launch_bounds__(kGvReduceCols * kGvReduceWaves)
+template <int DT, int W, int L>
+__global__ void __launch_bounds__(kGvReduceCols * W)
 gemm_gemv_reduce_kernel(const float* __restrict__ ws, uint16_t* __restrict__ C, int64_t mn, int splits) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int64_t i = (int64_t)blockIdx.x * kGvReduceCols + lane;
     float s = 0.f;
-    for (int p0 = 0; p0 < splits; p0 += kGvReduceWaves * kGvReduceLoads) {
-        float v[kGvReduceLoads];
+    for (int p0 = 0; p0 < splits; p0 += W * L) {
+        float v[L];
 #pragma unroll
-        for (int j = 0; j < kGvReduceLoads; ++j) {
-            const int p = p0 + wave + kGvReduceWaves * j;
+        for (int j = 0; j < L; ++j) {
+            const int p = p0 + wave + W * j;
             v[j] = (p < splits && i < mn) ? ws[(int64_t)p * mn + i] : 0.f;
         }
 #pragma unroll
-        for (int j = 0; j < kGvReduceLoads; ++j) s += v[j];
+        for (int j = 0; j < L; ++j) s += v[j];
     }
-    __shared__ float red[kGvReduceWaves][kGvReduceCols];
+    __shared__ float red[W][kGvReduceCols];
     red[wave][lane] = s;
     __syncthreads();
     if (wave != 0 || i >= mn) return;
     float t = red[0][lane];
 #pragma unroll
-    for (int w = 1; w < kGvReduceWaves; ++w) t += red[w][lane];
+    for (int w = 1; w < W; ++w) t += red[w][lane];
     C[i] = round16<DT>(t);
+}
+
+template <int DT>
+int launch_reduce(const float* ws, uint16_t* C, int64_t mn, int splits, hipStream_t stream) {
+    typedef void (*Reduce)(const float*, uint16_t*, int64_t, int);
+    Reduce reduce = gemm_gemv_reduce_kernel<DT, 16, 32>;
+    int waves = 16;
+    if (splits <= 4) reduce = gemm_gemv_reduce_kernel<DT, 4, 1>, waves = 4;
+    else if (splits <= 8) reduce = gemm_gemv_reduce_kernel<DT, 4, 2>, waves = 4;
+    else if (splits <= 16) reduce = gemm_gemv_reduce_kernel<DT, 4, 4>, waves = 4;
+    else if (splits <= 32) reduce = gemm_gemv_reduce_kernel<DT, 16, 2>;
+    else if (splits <= 64) reduce = gemm_gemv_reduce_kernel<DT, 16, 4>;
+    else if (splits <= 128) reduce = gemm_gemv_reduce_kernel<DT, 16, 8>;
+    else if (splits <= 256) reduce = gemm_gemv_reduce_kernel<DT, 16, 16>;
+    hipLaunchKernelGGL(reduce, dim3((unsigned)((mn + kGvReduceCols - 1) / kGvReduceCols)),
+                       dim3(kGvReduceCols * waves), 0, stream, ws, C, mn, splits);
+    MB_HIP_TRY(hipGetLastError());
+    return MB_OK;
 }
 
 template <int DT, int MR>
@@ -163,13 +184,7 @@ int launch_m(const void* A, const void* B, void* C, int64_t M, int64_t N, int64_
                        static_cast<const uint16_t*>(A), static_cast<const uint16_t*>(B), static_cast<uint16_t*>(C),
                        (int)N, (int)K, k_len, ws);
     MB_HIP_TRY(hipGetLastError());
-    if (splits > 1) {
-        const int64_t mn = M * N;
-        hipLaunchKernelGGL(gemm_gemv_reduce_kernel<DT>, dim3((unsigned)((mn + kGvReduceCols - 1) / kGvReduceCols)),
-                           dim3(kGvReduceCols * kGvReduceWaves), 0, stream, static_cast<const float*>(ws),
-                           static_cast<uint16_t*>(C), mn, splits);
-        MB_HIP_TRY(hipGetLastError());
-    }
+    if (splits > 1) return launch_reduce<DT>(ws, static_cast<uint16_t*>(C), M * N, splits, stream);
     return MB_OK;
 }
 
@@ -192,17 +207,27 @@ int launch_dt(const void* A, const void* B, void* C, int64_t M, int64_t N, int64
 int gemm_gemv_plan(int dtype, int64_t M, int64_t N, int64_t K, const DeviceProps& props, GemmPlan* plan) {
     if ((dtype != MB_DT_BFLOAT16 && dtype != MB_DT_FLOAT16) || M < 1 || M > kGvMaxM || N % 8 != 0 || K % 8 != 0)
         return MB_ERR_SHAPE;
-    if (K >= (int64_t(1) << 31) || N >= (int64_t(1) << 31)) return MB_ERR_SHAPE;
+    // The kernel's K and column indices are 32-bit: split starts (at most
+    // K + 8 x splits), the chunk loop's last step (128 rows past K) and the
+    // last block's columns (up to 248 past N) stay below 2^31.
+    if (K > (int64_t(1) << 31) - 8 * kGvMaxSplits - 256 || N > (int64_t(1) << 31) - 256) return MB_ERR_SHAPE;
     const int64_t cus = props.cu_count > 0 ? props.cu_count : 256;
     const int64_t groups = (N + kGvCols - 1) / kGvCols;
-    // Split K until the grid covers the GPU twice, keeping at least one chunk
-    // per half-wave in each split.
+    // Split K until the grid holds 8 blocks per CU (the loads they keep in
+    // flight are what streams B), keeping at least one chunk per half-wave in
+    // each split, the fp32 partials (splits x M x N x 4 bytes) within 1/16 of
+    // B's bytes (K x N x 2), since the reduction pass reads them back, and at
+    // most 512 splits, which that pass adds in one trip to memory. On MI355X
+    // with B from HBM, against 2 blocks per CU and no partials bound: 1 x 4096
+    // x 4096 10.5 -> 9.9 us (32 -> 64 splits), 1 x 8192 x 8192 28.3 -> 26.3
+    // (16 -> 64), 4 x 8192 x 8192 31.6 -> 29.3, 1 x 1024 x 8192 8.7 -> 7.9
+    // (128, reduction as above), 2 x 28672 x 4096 44.4 -> 44.2 (4 -> 16).
     int64_t splits = 1;
-    while (groups * splits * 2 <= 2 * cus && K / (splits * 2) >= kGvChunk * kGvHalfWaves && splits < 1024)
+    while (groups * splits * 2 <= 8 * cus && K / (splits * 2) >= kGvChunk * kGvHalfWaves &&
+           splits * 2 * 32 * M <= K && splits < kGvMaxSplits)
         splits *= 2;
     const int64_t force_splits = tuning(MB_TUNE_GEMM_SPLITS);
     if (force_splits >= 1) splits = force_splits;
-    if (splits > 65535) splits = 65535;
     plan->implementation = "gfx950_gemv_stream";
     plan->threads = kGvThreads;
     plan->grid = (int)(groups * splits);

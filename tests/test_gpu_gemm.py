@@ -185,7 +185,7 @@ def test_fp8_skinny_takes_128x128_tiles(lib, dtype):
 @pytest.mark.parametrize("shape", [(1, 4096, 4096), (16, 8192, 8192), (128, 8192, 8192), (100, 2048, 4096)])
 def test_skinny_shapes_split_k(lib, dtype, shape):
     # The skinny GEMM configurations: ragged M on the tiled kernel, K split
-    # over an fp32 workspace and summed by the split blocks that arrive last.
+    # over an fp32 workspace and summed by the reduction kernel.
     m, n, k = shape
     info = lib.gemm_info(capi.DTYPES[dtype], m, n, k)
     splits = info["split_k"]
@@ -443,11 +443,12 @@ def test_f32_lds_dma_constant_fill_is_exact(lib):
 @pytest.mark.parametrize("dtype", ["bfloat16", "float16"])
 @pytest.mark.parametrize("m", [1, 2, 3, 4])
 @pytest.mark.parametrize("nk", [(4096, 4096), (8, 8), (24, 1000), (1032, 72), (8192, 8192), (65544, 64),
-                                (256, 65536), (8, 131072)])
+                                (1024, 8192), (256, 65536), (8, 131072)])
 def test_small_m_stream_kernel(lib, dtype, m, nk):
     # M <= 4 streams B with fp32 FMAs; every element within the output rounding plus an fp32
     # accumulation bound of an fp64 brute force. 65544 x 64 keeps one K split (C written directly);
-    # 256 x 65536 and 8 x 131072 split K 512 ways, so the reduction adds its planes over 8 rounds.
+    # the others split K 4 to 512 ways (128 for 1 x 1024 x 8192, 512 for 256 x 65536 and 8 x 131072);
+    # with the forced 16, 32 and 256 splits below that covers each shape of the reduction pass.
     n, k = nk
     info = lib.gemm_info(capi.DTYPES[dtype], m, n, k)
     assert info["implementation"] == "gfx950_gemv_stream"
@@ -481,12 +482,13 @@ def test_small_m_one_split_writes_c_directly(lib):
     ("bfloat16", 3, 4, (128, 2048, 4096)), ("float16", 2, 8, (100, 1024, 8192)),
     ("float8_e4m3fn", 2, 4, (128, 1024, 8192)), ("bfloat16", 1, 2, (64, 2048, 2048)),
     ("bfloat16", -1, 16, (1, 4096, 4096)), ("float16", -1, 32, (3, 2048, 8192)),
+    ("float16", -1, 256, (2, 512, 65536)),
 ])
 def test_split_handoff_over_back_to_back_launches(lib, dtype, config, splits, shape, tune):
-    # The split blocks hand their partials to the tile's last arrival through one workspace that every
-    # launch reuses: 24 launches queued back to back on one stream, alternating two operand sets, each
-    # into its own C. A partial or arrival count carried over from an earlier launch, or a stale copy of
-    # the workspace in a cache, would make some C differ from its set's first result.
+    # The split blocks write their partials to one workspace that every launch reuses and the
+    # reduction kernel sums: 24 launches queued back to back on one stream, alternating two operand
+    # sets, each into its own C. A partial carried over from an earlier launch, or a stale copy of the
+    # workspace in a cache, would make some C differ from its set's first result.
     m, n, k = shape
     if config >= 0:
         tune(gemm_tiled_config=config)
