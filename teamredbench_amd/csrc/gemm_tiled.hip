@@ -1099,27 +1099,32 @@ int gemm_tiled_plan(int dtype, int64_t M, int64_t N, int64_t K, const DeviceProp
     // (1, 2, 4 .. 32, whole stages per split) that a cost model rates fastest:
     //   blocks  = tiles * s, in ceil(blocks / CUs) rounds;
     //   MFMA    = rounds x one block's 2 * BM * BN * K / s FLOP at a per-CU
-    //             rate of the configuration (4.57 / 3.67 / 2.64 TFLOP/s for
+    //             rate of the configuration (3.70 / 2.87 / 1.99 TFLOP/s for
     //             16-bit inputs, twice that for fp8);
-    //   stream  = the A and B bytes at 9.16 TB/s times the fraction of the
+    //   stream  = the A and B bytes at 6.26 TB/s times the fraction of the
     //             CUs the blocks occupy (each block keeps a fixed number of
     //             loads in flight, so too few blocks leave HBM idle);
     //   partials (s > 1): the fp32 partials written and read back at the
-    //             same rate, plus 7.1 us for the reduction pass;
-    //   time    = max(MFMA, stream) + rounds x 3.0 us (prologue, epilogue)
+    //             same rate, plus 4.72 us for the reduction pass;
+    //   time    = max(MFMA, stream) + rounds x 2.71 us (prologue, epilogue)
     //             + partials.
-    // The constants were fitted to 666 timings on MI355X (bf16, fp16, fp8
-    // e4m3; 45 shapes, M = 8..4096, N = 256..16384, K = 768..16384; every
-    // configuration x split 1..16) with B cycled through copies that exceed
-    // the 256 MB Infinity Cache, i.e. operands streamed from HBM. The
-    // model's pick is within 1.8% of the measured best in geometric mean
-    // (20% at worst); the previous model, fitted with B cache-resident,
-    // ran those shapes 9.7% (44% at worst) behind. 16 x 8192 x 8192 bf16:
-    // 4 splits on 128 x 128 tiles, 29.2 us against 35.5 for its 2.
+    // The constants minimise the measured cost of the model's pick, not its
+    // timing error (they are effective figures, not the part's rates), over
+    // 906 timings on MI355X (bf16, fp16, fp8 e4m3; 61 shapes, M = 8..4096,
+    // N = 256..16384, K = 768..16384; every configuration x split 1..16),
+    // with B cycled through copies that exceed the 256 MB Infinity Cache:
+    // the pick is within 0.65% of the measured best in geometric mean (11%
+    // at worst), against 1.8% (24%) for constants fitted to the timings
+    // themselves. On 48 further shapes where the two sets pick differently
+    // (splits up to 32), these picks ran 7.6% faster in geometric mean
+    // (0.89x - 1.39x): fp8 128 x 14336 x 8192 37.7 us on 128 x 128 tiles at
+    // 2 splits against 43.5 on 64 x 128 at 1, fp8 8 x 1024 x 2048 7.9 us at 32
+    // splits against 11.0 at 1, bf16 32 x 14336 x 8192 55.5 us at 4 splits
+    // against 49.4 at 2.
     int splits = 1;
     if (!fill_rule && (cfg < 0 || kConfigs[cfg].bm <= 128)) {
-        constexpr double kRate[4] = {0.0, 4.57e12, 3.67e12, 2.64e12}, kBw = 9.16e12, kRound = 2.99e-6,
-                         kReduce = 7.11e-6;
+        constexpr double kRate[4] = {0.0, 3.70e12, 2.87e12, 1.99e12}, kBw = 6.26e12, kRound = 2.71e-6,
+                         kReduce = 4.72e-6;
         int cands[3] = {1, 2, 3}, n_cands = 3, first = 0;
         if (cfg >= 0) cands[0] = cfg, n_cands = 1;
         else if (n128_only) first = 1;
