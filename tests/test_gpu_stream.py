@@ -145,3 +145,20 @@ def test_kernel_info_keys(lib):
     for key in ("implementation", "threads_per_block", "vector_unroll", "blocks_per_cu", "arch"):
         assert key in info
     assert info["arch"].startswith("gfx950")
+
+
+@pytest.mark.parametrize("mode, dtype, n, nontemporal", [
+    ("triad", "float32", 1 << 28, True),     # 3 GiB a pass: streams past the Infinity Cache
+    ("triad", "float32", 1 << 24, False),    # 192 MiB: fits, ordinary accesses keep it there
+    ("copy", "float32", 1 << 24, False),     # 128 MiB
+    ("copy", "bfloat16", 1 << 24, True),     # 64 MiB: below the window, the two hints measure alike
+    ("triad", "bfloat16", 1 << 24, False),   # 96 MiB, the window's lower edge
+    ("copy", "float32", 1 << 25, False),     # 256 MiB, its upper edge
+    ("triad", "float32", 1 << 25, True),     # 384 MiB
+    ("copy", "float32", 1 << 20, True),
+])
+def test_nontemporal_hint_follows_the_pass_size(lib, mode, dtype, n, nontemporal):
+    info = lib.stream_info(capi.OPS[mode], capi.DTYPES[dtype], n)
+    assert info["nontemporal"] is nontemporal, info
+    with lib.tuned(stream_nontemporal=0 if nontemporal else 1):    # the knob still overrides it
+        assert lib.stream_info(capi.OPS[mode], capi.DTYPES[dtype], n)["nontemporal"] is not nontemporal
