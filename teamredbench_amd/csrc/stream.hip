@@ -363,20 +363,22 @@ struct StreamTuning {
 // copy and scale (one read stream) 4.
 //
 // The nontemporal hint keeps the arrays out of the 256 MB Infinity Cache.
-// When one pass touches 96..256 MiB (reads plus writes), the arrays fit in it,
-// and a caller that makes repeated passes over the same arrays (a timed loop,
-// an iterative solver) finds them there with ordinary accesses: on MI355X,
-// median of 5 interleaved runs of 50 launches, fp32 / bf16 copy and triad ran
-// 5-12% faster at 96..224 MiB without the hint (fp32 triad at 192 MiB 6920
-// against 6467 GB/s) and 1.5-9% faster at 256 MiB, while above 256 MiB the
-// hint won by 8-10% (fp32 triad at 384 MiB 6512 against 5875) and at 64 MiB
-// and below the two were within noise of each other.
-constexpr uint64_t kCacheFitLo = uint64_t(96) << 20;
+// When one pass touches 64..256 MiB (reads plus writes; 80..256 MiB for the
+// triad's two read streams), the arrays fit in it, and a caller that makes
+// repeated passes over the same arrays (a timed loop, an iterative solver)
+// finds them there with ordinary accesses. On MI355X, medians of 5-9
+// interleaved runs of 50 launches: without the hint fp32 / bf16 copy ran 2%
+// faster at 64 MiB and 5-9% at 96..256 MiB, scale 6-11% from 64 MiB, triad
+// 1-3% at 80 MiB and 3-12% at 96..224 MiB (fp32 at 192 MiB 6920 against 6467
+// GB/s); below those sizes the hint was equal or better (triad by 3-5% at
+// 48..64 MiB), and above 256 MiB it won by 8-10% (fp32 triad at 384 MiB 6512
+// against 5875).
 constexpr uint64_t kCacheFitHi = uint64_t(256) << 20;
 
 StreamTuning default_tuning(int op, int dtype, uint64_t n) {
+    const uint64_t lo = (op == MB_OP_TRIAD ? uint64_t(80) : uint64_t(64)) << 20;
     const uint64_t touched = n <= kCacheFitHi ? (op == MB_OP_TRIAD ? 3u : 2u) * n * (uint64_t)dtype_size(dtype) : 0;
-    const bool nt = !(touched >= kCacheFitLo && touched <= kCacheFitHi);
+    const bool nt = !(touched >= lo && touched <= kCacheFitHi);
     if (op == MB_OP_TRIAD) return {1, 256, 2, nt, 0};
     return {1, 256, 4, nt, 0};
 }

@@ -151,9 +151,12 @@ def test_kernel_info_keys(lib):
     ("triad", "float32", 1 << 28, True),     # 3 GiB a pass: streams past the Infinity Cache
     ("triad", "float32", 1 << 24, False),    # 192 MiB: fits, ordinary accesses keep it there
     ("copy", "float32", 1 << 24, False),     # 128 MiB
-    ("copy", "bfloat16", 1 << 24, True),     # 64 MiB: below the window, the two hints measure alike
-    ("triad", "bfloat16", 1 << 24, False),   # 96 MiB, the window's lower edge
-    ("copy", "float32", 1 << 25, False),     # 256 MiB, its upper edge
+    ("copy", "bfloat16", 1 << 24, False),    # 64 MiB, the copy / scale window's lower edge
+    ("scale", "bfloat16", (1 << 24) - 8, True),   # just below it
+    ("triad", "float32", 6990507, False),    # 80 MiB + 4 bytes, the triad's lower edge
+    ("triad", "float32", 6990506, True),     # 8 bytes below it
+    ("copy", "float32", 1 << 25, False),     # 256 MiB, the upper edge
+    ("scale", "float32", (1 << 25) + 8, True),    # just above it
     ("triad", "float32", 1 << 25, True),     # 384 MiB
     ("copy", "float32", 1 << 20, True),
 ])
