@@ -68,10 +68,7 @@ constexpr int kStageK = 64;                  // bytes of K per row per stage
 // barrier (one wave per SIMD: nothing else would keep it busy). Two measured
 // best: against one, fp8 8192^3 +1.0%, 8192 x 1024 x 8192 +1.9%, 16-bit
 // shapes +0.3-0.5%; three and four lose on 128-row tiles.
-#ifndef MB_PRE_BARRIER_MFMA
-#define MB_PRE_BARRIER_MFMA 2
-#endif
-constexpr int kPreBarrierMfma = MB_PRE_BARRIER_MFMA;
+constexpr int kPreBarrierMfma = 2;
 
 __device__ __forceinline__ int swz_b16(int k) { return ((k << 2) ^ (k << 1)) & 15; }
 // fp8 B rows of 256 bytes (256 columns) and of 128 bytes (128 columns).
