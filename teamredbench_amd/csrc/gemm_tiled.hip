@@ -1155,15 +1155,18 @@ int gemm_tiled_plan(int dtype, int64_t M, int64_t N, int64_t K, const DeviceProp
         return MB_ERR_SHAPE;
     }
     const TiledConfig& c = kConfigs[cfg];
-    // fp8 takes v_mfma_scale_f32_16x16x128_f8f6f4 on the 256 x 256 and
-    // 128 x 256 tiles when every split holds an even number of stages (one
-    // MFMA spans two): 2.3-4.2% faster than the 32x32x64 kernel on MI355X at
-    // 4096^3-16384^3, equal at 8192 x 1024 x 8192. On 128 x 128 tiles (eight
-    // MFMAs per step) it ran 2-4% slower, so those keep 32x32x64.
-    // The gemm_fp8_mfma override (16 or 32) forces either.
+    // fp8 takes v_mfma_scale_f32_16x16x128_f8f6f4 on tiles of 128 rows or
+    // more when every split holds an even number of stages (one MFMA spans
+    // two): on MI355X 2.3-4.2% faster than the 32x32x64 kernel at 4096^3 -
+    // 16384^3 (256 x 256), 2.6-3.9% on 128 x 256 tiles, and on 128 x 128 tiles
+    // 2-5.5% faster on 8 of 10 shapes (2048^3 13.5 against 14.3 us, e4m3 and
+    // e5m2 alike), equal at 128 x 8192 x 8192 and 1% slower at 1024 x 1024 x
+    // 4096. The 64 x 128 tiles (two fragment rows per wave) keep 32x32x64:
+    // within 0.6% either way there. The gemm_fp8_mfma override (16 or 32)
+    // forces either.
     const int64_t mfma_force = tuning(MB_TUNE_GEMM_FP8_MFMA);
     const bool mi16 = e == 1 && (K / splits) % (2 * stage_k) == 0 &&
-                      (mfma_force == 16 || (mfma_force != 32 && c.bn == 256));
+                      (mfma_force == 16 || (mfma_force != 32 && c.bm >= 128));
     const int frag = mi16 ? 16 : 32;
     plan->implementation = mi16 ? "gfx950_mfma16_lds_dma" : "gfx950_mfma32_lds_dma";
     plan->threads = 64 * c.wgm * c.wgn;

@@ -35,11 +35,11 @@ UNIT = {"float32": 2.0**-24, "float64": 2.0**-53}
 
 
 def tiled_impl(dtype: str, k: int, info: dict) -> str:
-    """The tiled kernel a plan takes: fp8 runs v_mfma_scale_f32_16x16x128_f8f6f4 on 256 x 256 and
-    128 x 256 tiles when every split holds an even number of 64-byte stages, the 32x32 kernels
-    otherwise (the gemm_fp8_mfma override, 16 or 32, forces either)."""
+    """The tiled kernel a plan takes: fp8 runs v_mfma_scale_f32_16x16x128_f8f6f4 on tiles of 128 rows
+    or more when every split holds an even number of 64-byte stages, the 32x32 kernels otherwise
+    (the gemm_fp8_mfma override, 16 or 32, forces either)."""
     force = str(info["overrides"].get("gemm_fp8_mfma", ""))
-    big_tile = info["tile_n"] == 256
+    big_tile = info["tile_m"] >= 128
     if dtype.startswith("float8") and (k // info["split_k"]) % 128 == 0 and \
             (force == "16" or (force != "32" and big_tile)):
         return "gfx950_mfma16_lds_dma"
