@@ -115,17 +115,12 @@ int check_gemm_args(int dtype, const void* A, const void* B, void* C, int64_t M,
         set_error("null matrix pointer (A=%p B=%p C=%p)", A, B, C);
         return MB_ERR_INVALID_ARG;
     }
-    const int es = dtype_size(dtype);
     const uintptr_t mis = reinterpret_cast<uintptr_t>(A) | reinterpret_cast<uintptr_t>(B) |
                           reinterpret_cast<uintptr_t>(C);
     if ((mis & 15u) != 0) {
         set_error("GEMM operands must be 16-byte aligned (A=%p B=%p C=%p)", A, B, C);
         return MB_ERR_SHAPE;
     }
-    (void)M;
-    (void)N;
-    (void)K;
-    (void)es;
     if (plan.workspace > 0 && (workspace == nullptr || workspace_bytes < plan.workspace)) {
         set_error("GEMM %s %lldx%lldx%lld needs %zu workspace bytes (got %zu at %p)",
                   dtype_name(dtype), (long long)M, (long long)N, (long long)K, plan.workspace,
