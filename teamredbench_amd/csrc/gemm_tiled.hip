@@ -1,9 +1,11 @@
 // LDS-pipelined MFMA GEMM for gfx950: C = alpha * (A * B), A (M x K) and
 // B (K x N) row-major, fp32 accumulation, output bf16 (bf16 and fp8 e4m3 /
 // e5m2 inputs) or fp16 (fp16 inputs). Tiles of 256 x 256, 128 x 256,
-// 128 x 128 or 64 x 128. Takes shapes with N % BN == 0 and K a multiple of
-// the stage depth, any M (the rows of a partial last M tile read as zeros and
-// are not stored); everything else goes to the generic kernel.
+// 128 x 128 or 64 x 128. Takes shapes with B's rows on 16 bytes (N a multiple
+// of 8, of 16 for fp8) and K a multiple of the stage depth, any M: the rows
+// of a partial last M tile read as zeros, and the columns of a partial last N
+// tile read the start of B's next row (zeros past B's end); neither is
+// stored. Everything else goes to the generic kernel.
 //
 // Data path. A stage is 64 bytes of K per row. A is held two stages at a
 // time, as [BM rows][128 B] pair slots; B one stage at a time, as
@@ -271,7 +273,8 @@ __device__ __forceinline__ u32x2 pack4(float a, float b, float c, float d) {
 // CU stores its tile at about the same moment, so keeping those lines out of
 // L2 lets the burst drain faster (measured +0.6% at 8192^3, +1.8% at 4096^3,
 // +2.6% at fp8 8192 x 1024 x 8192). Rows at or past M (a partial last tile)
-// are not stored.
+// and 8-column chunks at or past N (a partial last tile of a ragged N, which
+// is a multiple of 8) are not stored.
 template <int WTM, int ROW_BYTES>
 __device__ __forceinline__ void store_staged_tile(const unsigned char* stage, unsigned char* C, int M, int N,
                                                   int row_base, int64_t col_base, int lane) {
@@ -283,6 +286,7 @@ __device__ __forceinline__ void store_staged_tile(const unsigned char* stage, un
     static_assert(STORES % BATCH == 0, "stores split into batches");
     const int c = lane % ROW_CHUNKS;
     const int r0 = lane / ROW_CHUNKS;
+    const bool col_in = col_base + 8 * c < N;
     int grow = row_base + r0;
     unsigned char* cptr = C + (int64_t)grow * ldc + col_base * 2 + c * 16;
 #pragma unroll
@@ -295,7 +299,7 @@ __device__ __forceinline__ void store_staged_tile(const unsigned char* stage, un
         }
 #pragma unroll
         for (int p = 0; p < BATCH; ++p) {
-            if (grow < M) __builtin_nontemporal_store(rows[p], reinterpret_cast<u32x4*>(cptr));
+            if (grow < M && col_in) __builtin_nontemporal_store(rows[p], reinterpret_cast<u32x4*>(cptr));
             grow += ROWS_PER_STORE;
             cptr += ROWS_PER_STORE * ldc;
         }
@@ -359,11 +363,15 @@ gemm_tiled_kernel(const unsigned char* __restrict__ A, const unsigned char* __re
 
     // Buffer resources over this block's A row panel and B column panel. The A
     // range stops at row M, so the rows of a last, partial tile read as zeros.
+    // The B range stops at B's last byte: in a partial last N tile (ragged N)
+    // the columns at or past N of a row read the start of the next row, which
+    // only reaches C columns that are not stored, and past the last row they
+    // read as zeros.
     const int a_rows = min(BM, M - tm * BM);
     const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<unsigned char*>(A) + (int64_t)tm * BM * lda, (short)0, a_rows * lda, kBufferFlags);
     const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<unsigned char*>(B) + (int64_t)tn * BN * E, (short)0, K * ldb, kBufferFlags);
+        const_cast<unsigned char*>(B) + (int64_t)tn * BN * E, (short)0, K * ldb - tn * BN * E, kBufferFlags);
 
     // Global byte offsets of this lane's 16-byte pieces (pair 0 / stage 0);
     // a pair advances A by 2 * kStageK bytes, a stage advances B by K_ROWS
@@ -625,7 +633,8 @@ gemm_tiled_kernel(const unsigned char* __restrict__ A, const unsigned char* __re
                 for (int g = 0; g < 4; ++g) {
                     const f32x16& v = acc[i][j];
                     const f32x4 q = {v[4 * g], v[4 * g + 1], v[4 * g + 2], v[4 * g + 3]};
-                    *reinterpret_cast<f32x4*>(prow + col0 + 32 * j + 8 * g) = q;
+                    // N is a multiple of 8: the 4 columns are all in C or all past it
+                    if (col0 + 32 * j + 8 * g < N) *reinterpret_cast<f32x4*>(prow + col0 + 32 * j + 8 * g) = q;
                 }
             }
         }
@@ -725,7 +734,7 @@ gemm_fp8_mi16_kernel(const unsigned char* __restrict__ A, const unsigned char* _
     const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<unsigned char*>(A) + (int64_t)tm * BM * lda, (short)0, a_rows * lda, kBufferFlags);
     const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<unsigned char*>(B) + (int64_t)tn * BN, (short)0, K * ldb, kBufferFlags);
+        const_cast<unsigned char*>(B) + (int64_t)tn * BN, (short)0, K * ldb - tn * BN, kBufferFlags);
 
     // DMA offsets: instruction q of a wave covers A rows 8 * (wave * A_INSTR
     // + q) .. +7 (whole 128-byte pair rows) and B rows RPI * (wave * B_INSTR +
@@ -958,7 +967,8 @@ gemm_fp8_mi16_kernel(const unsigned char* __restrict__ A, const unsigned char* _
             if (row0 + 16 * i >= M) continue;
             float* prow = part + (int64_t)(row0 + 16 * i) * N;
 #pragma unroll
-            for (int j = 0; j < FN; ++j) *reinterpret_cast<f32x4*>(prow + col0 + 16 * j) = acc[i][j];
+            for (int j = 0; j < FN; ++j)
+                if (col0 + 16 * j < N) *reinterpret_cast<f32x4*>(prow + col0 + 16 * j) = acc[i][j];
         }
     }
 }
@@ -1004,7 +1014,7 @@ template <int DT, int CFG>
 int launch_cfg(const void* A, const void* B, void* C, int64_t M, int64_t N, int64_t K, float alpha,
                const GemmPlan& plan, void* workspace, hipStream_t stream) {
     constexpr TiledConfig c = kConfigs[CFG];
-    const int tiles_m = (int)((M + c.bm - 1) / c.bm), tiles_n = (int)(N / c.bn);
+    const int tiles_m = (int)((M + c.bm - 1) / c.bm), tiles_n = (int)((N + c.bn - 1) / c.bn);
     const int splits = plan.split_k;
     float* ws = splits > 1 ? static_cast<float*>(workspace) : nullptr;
     const dim3 grid(tiles_m * tiles_n * splits), block(64 * c.wgm * c.wgn);
@@ -1057,25 +1067,34 @@ int gemm_tiled_plan(int dtype, int64_t M, int64_t N, int64_t K, const DeviceProp
                     GemmPlan* plan, const char** why) {
     const int64_t e = is_fp8(dtype) ? 1 : 2;
     const int64_t stage_k = kStageK / e;
-    // N in 256-column tiles, or in 128-column tiles (configuration 2).
-    const bool n128_only = N % 256 != 0;
-    if (N % 128 != 0) {
-        *why = "N is not a multiple of 128";
+    // B's rows must start on 16 bytes (N a multiple of 8, or of 16 for fp8)
+    // for the 16-byte DMA loads. N a multiple of 256 takes any tile width; a
+    // multiple of 128 only the 128-column tiles (configurations 2 and 3),
+    // which then cover N exactly. Any other N (ragged) takes any tile width,
+    // with a partial last column of tiles: its columns past N load the start
+    // of B's next row (or zeros past B's end) and are not stored.
+    if ((N * e) % 16 != 0) {
+        *why = e == 1 ? "N is not a multiple of 16" : "N is not a multiple of 8";
         return MB_ERR_SHAPE;
     }
+    const bool ragged_n = N % 128 != 0;
+    const bool n128_only = !ragged_n && N % 256 != 0;
     if (K % stage_k != 0) {
         *why = e == 1 ? "K is not a multiple of 64" : "K is not a multiple of 32";
         return MB_ERR_SHAPE;
     }
-    if (K * N * e >= (int64_t(1) << 31) || 256 * K * e >= (int64_t(1) << 31) || M >= (int64_t(1) << 31) ||
-        M * N >= (int64_t(1) << 31)) {
+    // 32-bit buffer offsets: B's rows (plus a partial tile's 256 columns past
+    // the last), a 256-row A panel, and the C / partial planes.
+    if ((K * N + 256) * e >= (int64_t(1) << 31) || 256 * K * e >= (int64_t(1) << 31) ||
+        M >= (int64_t(1) << 31) || M * N >= (int64_t(1) << 31)) {
         *why = "operand offsets exceed 32-bit buffer addressing (K*N or 256*K bytes, or M*N, >= 2^31)";
         return MB_ERR_SHAPE;
     }
     const int64_t cus = props.cu_count > 0 ? props.cu_count : 256;
-    auto tiles = [&](int i) { return ((M + kConfigs[i].bm - 1) / kConfigs[i].bm) * (N / kConfigs[i].bn); };
+    auto tiles = [&](int i) {
+        return ((M + kConfigs[i].bm - 1) / kConfigs[i].bm) * ((N + kConfigs[i].bn - 1) / kConfigs[i].bn);
+    };
     const int forced_cfg = (int)tuning(MB_TUNE_GEMM_TILED_CONFIG);  // -1 unless forced
-    // N % 256 != 0 leaves the 128-column tiles (configurations 2 and 3).
     const int pinned = forced_cfg >= 0 && n128_only && forced_cfg < 2 ? 2 : forced_cfg;
     int cfg = pinned >= 0 ? pinned : (!n128_only && tiles(0) >= cus && M % kConfigs[0].bm == 0) ? 0 : -1;
     // Last-round fill. 128 x 256 tiles run 7-14% below 256 x 256 per FLOP on
