@@ -1,4 +1,5 @@
-"""GEMM with a ragged N on the pipelined kernels (-m gpu).
+"""GEMM shapes off the tile grid (-m gpu): a ragged N on the pipelined kernels,
+and the bounds-checked kernel that takes what they cannot.
 
 N that is not a multiple of the tile width but keeps B's rows on 16 bytes (a
 multiple of 8 for 16-bit inputs, of 16 for fp8) runs the LDS-DMA kernels with
@@ -16,6 +17,11 @@ row (zeros past B's end) and are not stored. Each case checks
 
 Configurations are forced through the plan override so that every tile width
 meets a partial last tile, with and without K splits.
+
+Shapes whose B rows are not on 16 bytes (N odd, or not a multiple of 16 for
+fp8) or whose K is not a multiple of 64 bytes run the bounds-checked kernel
+(128 x 128 tiles, every global access checked); the same checks hold there,
+on its 16-byte and element-wise A paths, and on aligned shapes forced onto it.
 """
 from __future__ import annotations
 
@@ -101,3 +107,28 @@ def test_ragged_n_with_k_splits(lib, tune, dtype, config, splits, shape):
     tune(gemm_tiled_config=config, gemm_splits=splits)
     info = run_checked(lib, dtype, *shape, seed=10 * splits + config)
     assert info["implementation"] in PIPELINED and info["split_k"] == splits, info
+
+
+GENERIC = "gfx950_mfma_generic"
+# (dtype, (M, N, K)): B rows off 16 bytes, or K off 64 bytes, with and without 16-byte A rows.
+FALLBACKS = [
+    ("bfloat16", (300, 1001, 520)), ("bfloat16", (257, 4000, 1000)), ("bfloat16", (128, 50257, 256)),
+    ("bfloat16", (1, 7, 3)), ("float16", (33, 129, 65)), ("float16", (520, 2050, 1001)),
+    ("float8_e4m3fn", (200, 1000, 4000)), ("float8_e4m3fn", (130, 2048, 4000)), ("float8_e5m2", (77, 4104, 1000)),
+    ("float8_e5m2", (129, 257, 97)),
+]
+
+
+@pytest.mark.parametrize("dtype, shape", FALLBACKS)
+def test_shapes_off_the_pipelined_kernels(lib, dtype, shape):
+    info = run_checked(lib, dtype, *shape, seed=sum(shape))
+    assert info["implementation"] == GENERIC and info["fallback"] != "", info
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("shape", [(1, 1, 1), (7, 9, 11), (256, 256, 512), (129, 257, 96), (5, 3000, 8),
+                                   (300, 1008, 512), (1024, 1024, 1024)])
+def test_bounds_checked_kernel_forced(lib, tune, dtype, shape):
+    tune(gemm_force_generic=1)
+    info = run_checked(lib, dtype, *shape, seed=len(shape) + shape[0])
+    assert info["implementation"] == GENERIC, info
