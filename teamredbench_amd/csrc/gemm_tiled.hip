@@ -1,11 +1,13 @@
 // LDS-pipelined MFMA GEMM for gfx950: C = alpha * (A * B), A (M x K) and
 // B (K x N) row-major, fp32 accumulation, output bf16 (bf16 and fp8 e4m3 /
 // e5m2 inputs) or fp16 (fp16 inputs). Tiles of 256 x 256, 128 x 256,
-// 128 x 128 or 64 x 128. Takes shapes with B's rows on 16 bytes (N a multiple
-// of 8, of 16 for fp8) and K a multiple of the stage depth, any M: the rows
-// of a partial last M tile read as zeros, and the columns of a partial last N
-// tile read the start of B's next row (zeros past B's end); neither is
-// stored. Everything else goes to the generic kernel.
+// 128 x 128 or 64 x 128. Takes shapes with A's and B's rows on 16 bytes (K
+// and N multiples of 8, of 16 for fp8), any M: the rows of a partial last M
+// tile read as zeros, and the columns of a partial last N tile read the start
+// of B's next row (zeros past B's end); neither is stored. A K that is not a
+// multiple of the stage depth runs whole stages, its A pieces past K loaded as
+// zeros (the RAGGED_K instantiations) and B's rows past K lying past B's end.
+// Everything else goes to the bounds-checked kernel.
 //
 // Data path. A stage is 64 bytes of K per row. A is held two stages at a
 // time, as [BM rows][128 B] pair slots; B one stage at a time, as
@@ -306,7 +308,7 @@ __device__ __forceinline__ void store_staged_tile(const unsigned char* stage, un
     }
 }
 
-template <int DT, int BM, int BN, int WGM, int WGN, int NA, int NB, bool SCALED>
+template <int DT, int BM, int BN, int WGM, int WGN, int NA, int NB, bool SCALED, bool RAGGED_K = false>
 __global__ void __launch_bounds__(64 * WGM * WGN)
 gemm_tiled_kernel(const unsigned char* __restrict__ A, const unsigned char* __restrict__ B,
                   unsigned char* __restrict__ C, int M, int N, int K, float alpha, int tiles_m,
@@ -379,12 +381,13 @@ gemm_tiled_kernel(const unsigned char* __restrict__ A, const unsigned char* __re
     // whole 128-byte lines; the swizzle of those rows depends on q only
     // through its parity, so two vector offsets serve all q and the rest,
     // 16 * (q / 2) rows, is a uniform offset.
-    int a_voff[2], b_voff[B_INSTR];
+    int a_voff[2], a_kbyte[2], b_voff[B_INSTR];
 #pragma unroll
     for (int q = 0; q < 2; ++q) {
         const int lin = (wave * A_INSTR + q) * 1024 + lane * 16;   // LDS byte in the pair slot
         const int row = lin / (2 * kStageK), pchunk = (lin % (2 * kStageK)) >> 4;
-        a_voff[q] = row * lda + ((pchunk ^ swz_a2(row)) << 4);
+        a_kbyte[q] = (pchunk ^ swz_a2(row)) << 4;                  // K byte of the piece within its pair
+        a_voff[q] = row * lda + a_kbyte[q];
     }
 #pragma unroll
     for (int q = 0; q < B_INSTR; ++q) {
@@ -395,11 +398,16 @@ gemm_tiled_kernel(const unsigned char* __restrict__ A, const unsigned char* __re
     }
 
     // DMA instruction q of A pair `pair` into `slot`, and of B stage `kt`.
+    // RAGGED_K (K not a multiple of the stage): the A pieces at or past K load
+    // zeros (an offset past the buffer range), so the stages that run past K
+    // add nothing; B's rows past K lie past B's end and load zeros too.
     auto issue_a = [&](int pair, unsigned char* slot, auto idx) {
         constexpr int q = decltype(idx)::value;
         const unsigned base = (unsigned)(uintptr_t)(MB_LDS unsigned char*)slot;
-        lds_dma16(ra, base + (wave * A_INSTR + q) * 1024, a_voff[q & 1],
-                  k0 * E + pair * 2 * kStageK + 16 * (q >> 1) * lda);
+        const int kb = k0 * E + pair * 2 * kStageK;
+        int voff = a_voff[q & 1];
+        if constexpr (RAGGED_K) voff = a_kbyte[q & 1] < K * E - kb ? voff : (int)0x80000000u;
+        lds_dma16(ra, base + (wave * A_INSTR + q) * 1024, voff, kb + 16 * (q >> 1) * lda);
     };
     auto issue_b = [&](int kt, unsigned char* slot, auto idx) {
         constexpr int q = decltype(idx)::value;
@@ -682,7 +690,7 @@ __device__ __forceinline__ f32x4 mfma16_fp8(const i32x8& a, const i32x8& b, f32x
     return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, fmt, fmt, 0, 0, 0, 0);
 }
 
-template <int DT, int BM, int BN, int WGM, int WGN, int NA, int NB, bool SCALED>
+template <int DT, int BM, int BN, int WGM, int WGN, int NA, int NB, bool SCALED, bool RAGGED_K = false>
 __global__ void __launch_bounds__(64 * WGM * WGN)
 gemm_fp8_mi16_kernel(const unsigned char* __restrict__ A, const unsigned char* __restrict__ B,
                      unsigned char* __restrict__ C, int M, int N, int K, float alpha, int tiles_m, int tiles_n,
@@ -741,20 +749,25 @@ gemm_fp8_mi16_kernel(const unsigned char* __restrict__ A, const unsigned char* _
     // q) .. +RPI-1 of the stage. Both swizzles depend on q only through its
     // parity (the B rows of a wave share bit 4), so two vector offsets per
     // operand serve every q; the rest is a uniform offset.
-    int a_voff[2], b_voff[2];
+    int a_voff[2], a_kbyte[2], b_voff[2];
 #pragma unroll
     for (int q = 0; q < 2; ++q) {
         const int lin = (wave * A_INSTR + q) * 1024 + lane * 16;
         const int row = lin / (2 * kStageK), pchunk = (lin % (2 * kStageK)) >> 4;
-        a_voff[q] = row * lda + ((pchunk ^ swz_a2(row)) << 4);
+        a_kbyte[q] = (pchunk ^ swz_a2(row)) << 4;
+        a_voff[q] = row * lda + a_kbyte[q];
         const int blin = (wave * B_INSTR + q) * 1024 + lane * 16;
         const int brow = blin / B_ROW, bchunk = (blin % B_ROW) >> 4;
         b_voff[q] = brow * ldb + ((bchunk ^ swz_b8_mi16(brow, B_ROW)) << 4);
     }
+    // RAGGED_K: A pieces at or past K load zeros, as in gemm_tiled_kernel.
     auto issue_a = [&](int pair, unsigned char* slot, auto idx) {
         constexpr int q = decltype(idx)::value;
         const unsigned base = (unsigned)(uintptr_t)(MB_LDS unsigned char*)slot;
-        lds_dma16(ra, base + (wave * A_INSTR + q) * 1024, a_voff[q & 1], k0 + pair * 2 * kStageK + 16 * (q >> 1) * lda);
+        const int kb = k0 + pair * 2 * kStageK;
+        int voff = a_voff[q & 1];
+        if constexpr (RAGGED_K) voff = a_kbyte[q & 1] < K - kb ? voff : (int)0x80000000u;
+        lds_dma16(ra, base + (wave * A_INSTR + q) * 1024, voff, kb + 16 * (q >> 1) * lda);
     };
     auto issue_b = [&](int kt, unsigned char* slot, auto idx) {
         constexpr int q = decltype(idx)::value;
@@ -1026,16 +1039,25 @@ int launch_cfg(const void* A, const void* B, void* C, int64_t M, int64_t N, int6
     typedef void (*Kernel)(const unsigned char*, const unsigned char*, unsigned char*, int, int, int, float, int,
                            int, int, int, int, float*);
     const bool scaled = is_fp8(DT) && alpha != 1.0f && splits == 1;
-    Kernel kernel = gemm_tiled_kernel<DT, c.bm, c.bn, c.wgm, c.wgn, c.na, c.nb, false>;
-    if constexpr (is_fp8(DT)) {
-        if (plan.frag_m == 16)
-            kernel = scaled ? gemm_fp8_mi16_kernel<DT, c.bm, c.bn, c.wgm, c.wgn, c.na, c.nb, true>
-                            : gemm_fp8_mi16_kernel<DT, c.bm, c.bn, c.wgm, c.wgn, c.na, c.nb, false>;
-        else if (scaled)
-            kernel = gemm_tiled_kernel<DT, c.bm, c.bn, c.wgm, c.wgn, c.na, c.nb, true>;
-    }
+    // K not a multiple of splits x stage: every split runs k_len (whole
+    // stages), and the instantiations with RAGGED_K zero the A pieces past K.
+    const int64_t stage_k = kStageK / Traits<DT>::kElem;
+    const int64_t stages = (K + stage_k - 1) / stage_k;
+    const int64_t k_len = (stages + splits - 1) / splits * stage_k;   // the plan's split_k_len
+    const bool ragged_k = k_len * splits != K;
+    auto pick = [&](auto rk) -> Kernel {
+        constexpr bool RK = decltype(rk)::value;
+        if constexpr (is_fp8(DT)) {
+            if (plan.frag_m == 16)
+                return scaled ? gemm_fp8_mi16_kernel<DT, c.bm, c.bn, c.wgm, c.wgn, c.na, c.nb, true, RK>
+                              : gemm_fp8_mi16_kernel<DT, c.bm, c.bn, c.wgm, c.wgn, c.na, c.nb, false, RK>;
+            if (scaled) return gemm_tiled_kernel<DT, c.bm, c.bn, c.wgm, c.wgn, c.na, c.nb, true, RK>;
+        }
+        return gemm_tiled_kernel<DT, c.bm, c.bn, c.wgm, c.wgn, c.na, c.nb, false, RK>;
+    };
+    const Kernel kernel = ragged_k ? pick(std::true_type{}) : pick(std::false_type{});
     hipLaunchKernelGGL(kernel, grid, block, 0, stream, a, b, cp, (int)M, (int)N, (int)K, scaled ? alpha : 1.0f,
-                       tiles_m, tiles_n, c.group_m, splits, (int)(K / splits), ws);
+                       tiles_m, tiles_n, c.group_m, splits, (int)k_len, ws);
     MB_HIP_TRY(hipGetLastError());
     if (splits > 1) {
         const int64_t quads = M * N / 4;
@@ -1079,17 +1101,32 @@ int gemm_tiled_plan(int dtype, int64_t M, int64_t N, int64_t K, const DeviceProp
     }
     const bool ragged_n = N % 128 != 0;
     const bool n128_only = !ragged_n && N % 256 != 0;
-    if (K % stage_k != 0) {
-        *why = e == 1 ? "K is not a multiple of 64" : "K is not a multiple of 32";
+    // A's rows must start on 16 bytes too. K that is not a multiple of the
+    // stage (ragged) runs over k_pad, K rounded up to whole stages: the A
+    // pieces past K load zeros, and B's rows past K lie past B's end.
+    if ((K * e) % 16 != 0) {
+        *why = e == 1 ? "K is not a multiple of 16" : "K is not a multiple of 8";
         return MB_ERR_SHAPE;
     }
-    // 32-bit buffer offsets: B's rows (plus a partial tile's 256 columns past
-    // the last), a 256-row A panel, and the C / partial planes.
-    if ((K * N + 256) * e >= (int64_t(1) << 31) || 256 * K * e >= (int64_t(1) << 31) ||
+    const int64_t k_pad = (K + stage_k - 1) / stage_k * stage_k;
+    // 32-bit buffer offsets: B's rows up to k_pad (plus a partial tile's 256
+    // columns past the last), a 256-row A panel, and the C / partial planes.
+    if ((k_pad * N + 256) * e >= (int64_t(1) << 31) || 256 * k_pad * e >= (int64_t(1) << 31) ||
         M >= (int64_t(1) << 31) || M * N >= (int64_t(1) << 31)) {
         *why = "operand offsets exceed 32-bit buffer addressing (K*N or 256*K bytes, or M*N, >= 2^31)";
         return MB_ERR_SHAPE;
     }
+    // K splits. A whole-stage K splits into s parts of K / s when they are
+    // whole stages. A ragged K splits into ceil(stages / s) stages each, the
+    // last split running furthest past K, for any s up to the stage count
+    // whose rows stay within 32-bit offsets.
+    const bool ragged_k = k_pad != K;
+    const int64_t stages = k_pad / stage_k;
+    auto split_ok = [&](int64_t sp) {
+        if (!ragged_k) return K % (stage_k * sp) == 0;
+        return sp <= stages && ((stages + sp - 1) / sp * sp * stage_k * N + 256) * e < (int64_t(1) << 31);
+    };
+    auto split_k_len = [&](int64_t sp) { return (stages + sp - 1) / sp * stage_k; };
     const int64_t cus = props.cu_count > 0 ? props.cu_count : 256;
     auto tiles = [&](int i) {
         return ((M + kConfigs[i].bm - 1) / kConfigs[i].bm) * ((N + kConfigs[i].bn - 1) / kConfigs[i].bn);
@@ -1150,10 +1187,10 @@ int gemm_tiled_plan(int dtype, int64_t M, int64_t N, int64_t K, const DeviceProp
             const double bm = kConfigs[c].bm, bn = kConfigs[c].bn;
             const double rate = kRate[c] * (e == 1 ? 2.0 : 1.0);
             for (int64_t sp = 1; sp <= 32; sp *= 2) {
-                if (K % (stage_k * sp) != 0) continue;
+                if (!split_ok(sp)) continue;
                 const double blocks = (double)(tiles(c) * sp);
                 const double rounds = std::ceil(blocks / (double)cus);
-                const double mfma = rounds * 2.0 * bm * bn * ((double)K / (double)sp) / rate;
+                const double mfma = rounds * 2.0 * bm * bn * (double)split_k_len(sp) / rate;
                 const double occupancy = blocks < (double)cus ? blocks / (double)cus : 1.0;
                 const double stream = (double)((K * N + M * K) * e) / (kBw * occupancy);
                 const double partials = sp > 1 ? 2.0 * (double)sp * (double)M * (double)N * 4.0 / kBw + kReduce : 0.0;
@@ -1167,7 +1204,7 @@ int gemm_tiled_plan(int dtype, int64_t M, int64_t N, int64_t K, const DeviceProp
         }
     }
     const int64_t force_splits = tuning(MB_TUNE_GEMM_SPLITS);
-    if (force_splits >= 1 && K % (stage_k * force_splits) == 0) splits = (int)force_splits;
+    if (force_splits >= 1 && split_ok(force_splits)) splits = (int)force_splits;
     if (kConfigs[cfg].bm > 128) splits = 1;   // the 256-row kernels carry no split path
     if (tiles(cfg) * splits > INT32_MAX) {
         *why = "more than 2^31 tiles";
@@ -1184,7 +1221,7 @@ int gemm_tiled_plan(int dtype, int64_t M, int64_t N, int64_t K, const DeviceProp
     // within 0.6% either way there. The gemm_fp8_mfma override (16 or 32)
     // forces either.
     const int64_t mfma_force = tuning(MB_TUNE_GEMM_FP8_MFMA);
-    const bool mi16 = e == 1 && (K / splits) % (2 * stage_k) == 0 &&
+    const bool mi16 = e == 1 && (split_k_len(splits) / stage_k) % 2 == 0 &&
                       (mfma_force == 16 || (mfma_force != 32 && c.bm >= 128));
     const int frag = mi16 ? 16 : 32;
     plan->implementation = mi16 ? "gfx950_mfma16_lds_dma" : "gfx950_mfma32_lds_dma";

@@ -627,7 +627,9 @@ def test_overrides_are_reported_and_the_environment_is_ignored(lib, tune, monkey
     ("bfloat16", (256, 196, 256), "gfx950_mfma_generic", "N is not a multiple of 8"),
     ("float8_e4m3fn", (256, 200, 256), "gfx950_mfma_generic", "N is not a multiple of 16"),
     ("bfloat16", (256, 200, 256), "gfx950_mfma32_lds_dma", ""),
-    ("float8_e4m3fn", (256, 256, 96), "gfx950_mfma_generic", "K is not a multiple of 64"),
+    ("float8_e4m3fn", (256, 256, 100), "gfx950_mfma_generic", "K is not a multiple of 16"),
+    ("bfloat16", (256, 256, 100), "gfx950_mfma_generic", "K is not a multiple of 8"),
+    ("float8_e4m3fn", (256, 256, 96), "gfx950_mfma32_lds_dma", ""),
     ("float32", (300, 200, 64), "gfx950_mfma_f32_32x32x2", "M or N is not a multiple of 128"),
     ("bfloat16", (256, 256, 256), "gfx950_mfma32_lds_dma", ""),
 ])

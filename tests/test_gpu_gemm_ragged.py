@@ -1,5 +1,5 @@
-"""GEMM shapes off the tile grid (-m gpu): a ragged N on the pipelined kernels,
-and the bounds-checked kernel that takes what they cannot.
+"""GEMM shapes off the tile grid (-m gpu): a ragged N or K on the pipelined
+kernels, and the bounds-checked kernel that takes what they cannot.
 
 N that is not a multiple of the tile width but keeps B's rows on 16 bytes (a
 multiple of 8 for 16-bit inputs, of 16 for fp8) runs the LDS-DMA kernels with
@@ -18,8 +18,13 @@ row (zeros past B's end) and are not stored. Each case checks
 Configurations are forced through the plan override so that every tile width
 meets a partial last tile, with and without K splits.
 
-Shapes whose B rows are not on 16 bytes (N odd, or not a multiple of 16 for
-fp8) or whose K is not a multiple of 64 bytes run the bounds-checked kernel
+A K that is not a multiple of the stage depth (64 bytes) but keeps A's rows on
+16 bytes runs the same kernels over whole stages, the A pieces past K loaded
+as zeros; the same checks hold, with the last split of a split-K plan running
+past K, and with N ragged too.
+
+Shapes whose A or B rows are not on 16 bytes (K or N not a multiple of 8, of
+16 for fp8) run the bounds-checked kernel
 (128 x 128 tiles, every global access checked); the same checks hold there,
 on its 16-byte and element-wise A paths, and on aligned shapes forced onto it.
 """
@@ -109,12 +114,44 @@ def test_ragged_n_with_k_splits(lib, tune, dtype, config, splits, shape):
     assert info["implementation"] in PIPELINED and info["split_k"] == splits, info
 
 
+# (M, N, K): K a multiple of 16 but not of 64 (fp8) / of 8 but not of 32 (16-bit), N ragged in some.
+RAGGED_K = [(256, 256, 80), (300, 1024, 1040), (1024, 4096, 4000), (128, 8000, 2064), (64, 144, 4112),
+            (520, 4112, 272)]
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("shape", RAGGED_K)
+def test_ragged_k_takes_the_pipelined_kernel(lib, dtype, shape):
+    info = run_checked(lib, dtype, *shape, seed=7)
+    assert info["implementation"] in PIPELINED and info["fallback"] == "", info
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("config", [0, 1, 2, 3])
+@pytest.mark.parametrize("shape", RAGGED_K[:4])
+def test_ragged_k_on_every_tile_configuration(lib, tune, dtype, config, shape):
+    tune(gemm_tiled_config=config, gemm_splits=1)
+    info = run_checked(lib, dtype, *shape, seed=config + 3)
+    assert info["implementation"] in PIPELINED and info["split_k"] == 1, info
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("config", [1, 2, 3])
+@pytest.mark.parametrize("splits", [2, 4, 8])
+@pytest.mark.parametrize("shape", [(128, 8000, 2064), (64, 144, 4112), (300, 1024, 1040)])
+def test_ragged_k_with_k_splits(lib, tune, dtype, config, splits, shape):
+    # The last split runs past K (a whole stage of zeros at 8 splits of 1040 bf16 K), the others are full.
+    tune(gemm_tiled_config=config, gemm_splits=splits)
+    info = run_checked(lib, dtype, *shape, seed=20 * splits + config)
+    assert info["implementation"] in PIPELINED and info["split_k"] == splits, info
+
+
 GENERIC = "gfx950_mfma_generic"
-# (dtype, (M, N, K)): B rows off 16 bytes, or K off 64 bytes, with and without 16-byte A rows.
+# (dtype, (M, N, K)): B rows off 16 bytes, or A rows off 16 bytes (K not a multiple of 8 / 16).
 FALLBACKS = [
-    ("bfloat16", (300, 1001, 520)), ("bfloat16", (257, 4000, 1000)), ("bfloat16", (128, 50257, 256)),
+    ("bfloat16", (300, 1001, 520)), ("bfloat16", (257, 4000, 1001)), ("bfloat16", (128, 50257, 256)),
     ("bfloat16", (1, 7, 3)), ("float16", (33, 129, 65)), ("float16", (520, 2050, 1001)),
-    ("float8_e4m3fn", (200, 1000, 4000)), ("float8_e4m3fn", (130, 2048, 4000)), ("float8_e5m2", (77, 4104, 1000)),
+    ("float8_e4m3fn", (200, 1000, 4000)), ("float8_e4m3fn", (130, 2048, 4001)), ("float8_e5m2", (77, 4104, 1000)),
     ("float8_e5m2", (129, 257, 97)),
 ]
 
