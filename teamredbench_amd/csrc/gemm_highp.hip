@@ -235,7 +235,7 @@ constexpr int kF32Stages = 4, kF32StageK = 16, kF32GroupM = 4;
 
 __device__ __forceinline__ int swz_b32(int row) { return ((row >> 3) & 1) << 3; }
 
-template <int BM, int BN>
+template <int BM, int BN, bool RAGGED_K = false>
 __global__ void __launch_bounds__(256)
 gemm_f32_dma_kernel(const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ C, int M, int N,
                     int K, int tiles_m, int tiles_n) {
@@ -251,16 +251,20 @@ gemm_f32_dma_kernel(const float* __restrict__ A, const float* __restrict__ B, fl
     int tm, tn;
     tile_coords((int)blockIdx.x, tiles_m * tiles_n, tiles_m, tiles_n, kF32GroupM, &tm, &tn);
     const int lda = K * 4, ldb = N * 4;
+    // Buffer ranges end at A's row M and at B's last byte: rows of a partial
+    // last M tile, and B's rows past K, load zeros; the columns of a partial
+    // last N tile load the start of B's next row and are not stored.
     const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<float*>(A) + (int64_t)tm * BM * K, (short)0, BM * lda, kBufferFlags);
+        const_cast<float*>(A) + (int64_t)tm * BM * K, (short)0, min(BM, M - tm * BM) * lda, kBufferFlags);
     const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<float*>(B) + (int64_t)tn * BN, (short)0, K * ldb, kBufferFlags);
-    int a_voff[AInstr], b_voff[BInstr];
+        const_cast<float*>(B) + (int64_t)tn * BN, (short)0, K * ldb - tn * BN * 4, kBufferFlags);
+    int a_voff[AInstr], a_kbyte[AInstr], b_voff[BInstr];
 #pragma unroll
     for (int q = 0; q < AInstr; ++q) {
         const int lin = (wave * AInstr + q) * 1024 + lane * 16;
         const int row = lin / 64, pchunk = (lin % 64) >> 4;
-        a_voff[q] = row * lda + ((pchunk ^ swz_a(row)) << 4);
+        a_kbyte[q] = (pchunk ^ swz_a(row)) << 4;
+        a_voff[q] = row * lda + a_kbyte[q];
     }
 #pragma unroll
     for (int q = 0; q < BInstr; ++q) {
@@ -270,9 +274,11 @@ gemm_f32_dma_kernel(const float* __restrict__ A, const float* __restrict__ B, fl
     }
     auto issue = [&](int kt, int slot) {
         const unsigned base = (unsigned)(uintptr_t)(MB_LDS unsigned char*)ring[slot];
+        // RAGGED_K (K not a multiple of the stage): A pieces at or past K load zeros.
 #pragma unroll
         for (int q = 0; q < AInstr; ++q)
-            lds_dma16(ra, base + (wave * AInstr + q) * 1024, a_voff[q], kt * 64);
+            lds_dma16(ra, base + (wave * AInstr + q) * 1024,
+                      RAGGED_K && a_kbyte[q] >= K * 4 - kt * 64 ? (int)0x80000000u : a_voff[q], kt * 64);
 #pragma unroll
         for (int q = 0; q < BInstr; ++q)
             lds_dma16(rb, base + ABytes + (wave * BInstr + q) * 1024, b_voff[q], kt * kF32StageK * ldb);
@@ -286,7 +292,7 @@ gemm_f32_dma_kernel(const float* __restrict__ A, const float* __restrict__ B, fl
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
-    const int ksteps = K / kF32StageK, last = ksteps - 1;
+    const int ksteps = (K + kF32StageK - 1) / kF32StageK, last = ksteps - 1;
 #pragma unroll
     for (int st = 0; st < kF32Stages - 1; ++st) issue(min(st, last), st);
     const int a_row = wm * WTM + (lane & 31);
@@ -356,16 +362,19 @@ gemm_f32_dma_kernel(const float* __restrict__ A, const float* __restrict__ B, fl
 
     // Accumulator register 4g + q of lane l holds C[row 32i + l % 32]
     // [col 32j + 8g + 4 * (l / 32) + q] of the wave's tile.
+    // Rows at or past M and 4-column groups at or past N (a multiple of 4) are not stored.
+    const int col0 = tn * BN + wn * WTN + 4 * half;
 #pragma unroll
     for (int i = 0; i < FM; ++i) {
-        float* crow = C + (int64_t)(tm * BM + wm * WTM + 32 * i + (lane & 31)) * N + tn * BN + wn * WTN +
-                      4 * half;
+        const int row = tm * BM + wm * WTM + 32 * i + (lane & 31);
+        if (row >= M) continue;
+        float* crow = C + (int64_t)row * N + col0;
 #pragma unroll
         for (int j = 0; j < FN; ++j)
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
                 const f32x4 v = {acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]};
-                *reinterpret_cast<f32x4*>(crow + 32 * j + 8 * g) = v;
+                if (col0 + 32 * j + 8 * g < N) *reinterpret_cast<f32x4*>(crow + 32 * j + 8 * g) = v;
             }
     }
 }
@@ -387,7 +396,7 @@ constexpr int kF64Stages = 4, kF64StageK = 8;
 
 __device__ __forceinline__ int swz_b64(int row) { return ((row >> 1) & 1) << 3; }
 
-template <int BM, int BN>
+template <int BM, int BN, bool RAGGED_K = false>
 __global__ void __launch_bounds__(256)
 gemm_f64_dma_kernel(const double* __restrict__ A, const double* __restrict__ B, double* __restrict__ C, int M,
                     int N, int K, int tiles_m, int tiles_n) {
@@ -403,16 +412,18 @@ gemm_f64_dma_kernel(const double* __restrict__ A, const double* __restrict__ B, 
     int tm, tn;
     tile_coords((int)blockIdx.x, tiles_m * tiles_n, tiles_m, tiles_n, kF32GroupM, &tm, &tn);
     const int lda = K * 8, ldb = N * 8;
+    // Buffer ranges as in gemm_f32_dma_kernel: partial last tiles and a ragged K.
     const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<double*>(A) + (int64_t)tm * BM * K, (short)0, BM * lda, kBufferFlags);
+        const_cast<double*>(A) + (int64_t)tm * BM * K, (short)0, min(BM, M - tm * BM) * lda, kBufferFlags);
     const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<double*>(B) + (int64_t)tn * BN, (short)0, K * ldb, kBufferFlags);
-    int a_voff[AInstr], b_voff[BInstr];
+        const_cast<double*>(B) + (int64_t)tn * BN, (short)0, K * ldb - tn * BN * 8, kBufferFlags);
+    int a_voff[AInstr], a_kbyte[AInstr], b_voff[BInstr];
 #pragma unroll
     for (int q = 0; q < AInstr; ++q) {
         const int lin = (wave * AInstr + q) * 1024 + lane * 16;
         const int row = lin / 64, pchunk = (lin % 64) >> 4;
-        a_voff[q] = row * lda + ((pchunk ^ swz_a(row)) << 4);
+        a_kbyte[q] = (pchunk ^ swz_a(row)) << 4;
+        a_voff[q] = row * lda + a_kbyte[q];
     }
 #pragma unroll
     for (int q = 0; q < BInstr; ++q) {
@@ -424,7 +435,8 @@ gemm_f64_dma_kernel(const double* __restrict__ A, const double* __restrict__ B, 
         const unsigned base = (unsigned)(uintptr_t)(MB_LDS unsigned char*)ring[slot];
 #pragma unroll
         for (int q = 0; q < AInstr; ++q)
-            lds_dma16(ra, base + (wave * AInstr + q) * 1024, a_voff[q], kt * 64);
+            lds_dma16(ra, base + (wave * AInstr + q) * 1024,
+                      RAGGED_K && a_kbyte[q] >= K * 8 - kt * 64 ? (int)0x80000000u : a_voff[q], kt * 64);
 #pragma unroll
         for (int q = 0; q < BInstr; ++q)
             lds_dma16(rb, base + ABytes + (wave * BInstr + q) * 1024, b_voff[q], kt * kF64StageK * ldb);
@@ -438,7 +450,7 @@ gemm_f64_dma_kernel(const double* __restrict__ A, const double* __restrict__ B, 
 #pragma unroll
             for (int r = 0; r < 4; ++r) acc[i][j][r] = 0.0;
 
-    const int ksteps = K / kF64StageK, last = ksteps - 1;
+    const int ksteps = (K + kF64StageK - 1) / kF64StageK, last = ksteps - 1;
 #pragma unroll
     for (int st = 0; st < kF64Stages - 1; ++st) issue(min(st, last), st);
     const int a_row = wm * WTM + (lane & 15);
@@ -498,41 +510,58 @@ gemm_f64_dma_kernel(const double* __restrict__ A, const double* __restrict__ B, 
     }
     wait_vmcnt_and_barrier<0>();
 
+    // Rows at or past M and columns at or past N are not stored.
+    const int col0 = tn * BN + wn * WTN + (lane & 15);
 #pragma unroll
     for (int i = 0; i < FM; ++i)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            double* crow = C + (int64_t)(tm * BM + wm * WTM + 16 * i + 4 * r + grp) * N + tn * BN + wn * WTN +
-                           (lane & 15);
+            const int row = tm * BM + wm * WTM + 16 * i + 4 * r + grp;
+            if (row >= M) continue;
+            double* crow = C + (int64_t)row * N + col0;
 #pragma unroll
-            for (int j = 0; j < FN; ++j) crow[16 * j] = acc[i][j][r];
+            for (int j = 0; j < FN; ++j)
+                if (col0 + 16 * j < N) crow[16 * j] = acc[i][j][r];
         }
 }
 
 // Which LDS-DMA ring a shape takes: 1 = the large tile (fp32 256 x 256, fp64
 // 256 x 128) when its tiles cover every CU, 2 = 128 x 128 when the shape
-// divides into it (2048^3 makes 64 large tiles but 256 small ones), 0 = the
-// register-staged kernel, with *why naming the reason. K must be whole stages
-// and the buffer offsets (B's K x N bytes, a 256-row A panel) must stay
-// within 31 bits.
+// divides into it (2048^3 makes 64 large tiles but 256 small ones); a shape
+// that divides into neither takes partial last tiles, on the large tile when
+// those cover every CU. 0 = the register-staged kernel, with *why naming the
+// reason: A's or B's rows not on 16 bytes, or buffer offsets (B's K x N bytes,
+// a 256-row A panel) beyond 31 bits. A K that is not whole stages runs the
+// RAGGED_K instantiations, whose A pieces past K load zeros.
 int highp_dma_config(bool f64, int64_t M, int64_t N, int64_t K, int cus, const char** why) {
     if (tuning(MB_TUNE_GEMM_HIGHP_STAGED) == 1) {
         *why = "forced by the gemm_highp_staged override";
         return 0;
     }
     const int64_t e = f64 ? 8 : 4, stage_k = f64 ? kF64StageK : kF32StageK;
-    if (K % stage_k != 0) {
-        *why = f64 ? "K is not a multiple of 8" : "K is not a multiple of 16";
+    // The DMA loads need A's and B's rows on 16 bytes.
+    if ((K * e) % 16 != 0) {
+        *why = f64 ? "K is not a multiple of 2" : "K is not a multiple of 4";
         return 0;
     }
-    if (K * N * e >= (int64_t(1) << 31) || 256 * K * e >= (int64_t(1) << 31)) {
+    if ((N * e) % 16 != 0) {
+        *why = f64 ? "N is not a multiple of 2" : "N is not a multiple of 4";
+        return 0;
+    }
+    const int64_t k_pad = (K + stage_k - 1) / stage_k * stage_k;
+    if ((k_pad * N + 256) * e >= (int64_t(1) << 31) || 256 * k_pad * e >= (int64_t(1) << 31)) {
         *why = "operand offsets exceed 32-bit buffer addressing (K*N or 256*K bytes >= 2 GiB)";
         return 0;
     }
     const int64_t bm = 256, bn = f64 ? 128 : 256;
-    if (M % bm == 0 && N % bn == 0 && (M / bm) * (N / bn) >= cus && (M / bm) * (N / bn) <= INT32_MAX) return 1;
-    if (M % 128 == 0 && N % 128 == 0 && (M / 128) * (N / 128) <= INT32_MAX) return 2;
-    *why = "M or N is not a multiple of 128";
+    auto tiles = [&](int64_t tm, int64_t tn) { return ((M + tm - 1) / tm) * ((N + tn - 1) / tn); };
+    const bool fits_large = tiles(bm, bn) >= cus && tiles(bm, bn) <= INT32_MAX;
+    if (M % bm == 0 && N % bn == 0 && fits_large) return 1;
+    if (M % 128 == 0 && N % 128 == 0 && tiles(128, 128) <= INT32_MAX) return 2;
+    // Ragged M or N: partial last tiles, the large tile when its tiles cover every CU.
+    if (fits_large) return 1;
+    if (tiles(128, 128) <= INT32_MAX) return 2;
+    *why = "more than 2^31 tiles";
     return 0;
 }
 
@@ -543,16 +572,17 @@ void highp_dma_tile(bool f64, int cfg, int* bm, int* bn) {
 
 template <typename T, int BM, int BN>
 int launch_dma(const void* A, const void* B, void* C, int64_t M, int64_t N, int64_t K, hipStream_t stream) {
-    const int tiles_m = (int)(M / BM), tiles_n = (int)(N / BN);
+    const int tiles_m = (int)((M + BM - 1) / BM), tiles_n = (int)((N + BN - 1) / BN);
     const T* a = static_cast<const T*>(A);
     const T* b = static_cast<const T*>(B);
     T* c = static_cast<T*>(C);
+    const dim3 grid(tiles_m * tiles_n);
     if constexpr (sizeof(T) == 4) {
-        hipLaunchKernelGGL((gemm_f32_dma_kernel<BM, BN>), dim3(tiles_m * tiles_n), dim3(256), 0, stream, a, b, c,
-                           (int)M, (int)N, (int)K, tiles_m, tiles_n);
+        auto kernel = K % kF32StageK != 0 ? gemm_f32_dma_kernel<BM, BN, true> : gemm_f32_dma_kernel<BM, BN, false>;
+        hipLaunchKernelGGL(kernel, grid, dim3(256), 0, stream, a, b, c, (int)M, (int)N, (int)K, tiles_m, tiles_n);
     } else {
-        hipLaunchKernelGGL((gemm_f64_dma_kernel<BM, BN>), dim3(tiles_m * tiles_n), dim3(256), 0, stream, a, b, c,
-                           (int)M, (int)N, (int)K, tiles_m, tiles_n);
+        auto kernel = K % kF64StageK != 0 ? gemm_f64_dma_kernel<BM, BN, true> : gemm_f64_dma_kernel<BM, BN, false>;
+        hipLaunchKernelGGL(kernel, grid, dim3(256), 0, stream, a, b, c, (int)M, (int)N, (int)K, tiles_m, tiles_n);
     }
     MB_HIP_TRY(hipGetLastError());
     return MB_OK;
@@ -585,7 +615,7 @@ int gemm_highp_plan(int dtype, int64_t M, int64_t N, int64_t K, const DeviceProp
         highp_dma_tile(f64, cfg, &bm, &bn);
         plan->implementation = f64 ? "gfx950_mfma_f64_16x16x4_lds_dma" : "gfx950_mfma_f32_32x32x2_lds_dma";
         plan->threads = 256;
-        plan->grid = (int)((M / bm) * (N / bn));
+        plan->grid = (int)(((M + bm - 1) / bm) * ((N + bn - 1) / bn));
         plan->tile_m = bm;
         plan->tile_n = bn;
         plan->tile_k = f64 ? kF64StageK : kF32StageK;

@@ -345,19 +345,25 @@ def test_highp_against_float64_brute_force(lib, dtype, shape):
 
 @pytest.mark.parametrize("dtype", HIGHP)
 def test_highp_kernel_info(lib, dtype):
+    # 1000^3 takes the LDS-DMA ring with partial last tiles and a ragged K; 1001 columns (rows off
+    # 16 bytes) the register-staged kernel
     info = lib.gemm_info(capi.DTYPES[dtype], 1000, 1000, 1000)
-    assert info["implementation"] == {"float32": "gfx950_mfma_f32_32x32x2", "float64": "gfx950_mfma_f64_16x16x4"}[dtype]
+    assert info["implementation"] == {"float32": "gfx950_mfma_f32_32x32x2_lds_dma",
+                                      "float64": "gfx950_mfma_f64_16x16x4_lds_dma"}[dtype]
     assert info["workspace_bytes"] == 0 and info["tile_m"] == 128
+    info = lib.gemm_info(capi.DTYPES[dtype], 1000, 1001, 1000)
+    assert info["implementation"] == {"float32": "gfx950_mfma_f32_32x32x2", "float64": "gfx950_mfma_f64_16x16x4"}[dtype]
 
 
 @pytest.mark.parametrize("shape, tile", [((4096, 4096, 64), (256, 256)), ((8192, 2048, 96), (256, 256)),
                                          ((4352, 4096, 16), (256, 256)), ((2048, 2048, 2048), (128, 128)),
-                                         ((1024, 1536, 48), (128, 128)), ((4096, 4096, 40), None),
-                                         ((4096, 4000, 64), None)])
+                                         ((1024, 1536, 48), (128, 128)), ((4096, 4096, 40), (256, 256)),
+                                         ((4096, 4000, 64), (256, 256)), ((1000, 1000, 64), (128, 128)),
+                                         ((4096, 4001, 64), None), ((4096, 4096, 42), None)])
 def test_f32_lds_dma_kernel_selection(lib, shape, tile):
     # fp32 takes the LDS-DMA ring with 256 x 256 tiles when they cover every CU, else with 128 x 128
-    # tiles when the shape divides (2048^3: 64 large tiles, 256 small); K must be whole stages of 16.
-    # Other shapes keep the register-staged kernel.
+    # tiles when the shape divides (2048^3: 64 large tiles, 256 small), else on partial last tiles; a K
+    # off the 16-deep stage runs whole stages. Rows of A or B off 16 bytes keep the register-staged kernel.
     info = lib.gemm_info(capi.DT_FLOAT32, *shape)
     if tile is None:
         assert info["implementation"] == "gfx950_mfma_f32_32x32x2" and info["tile_m"] == 128
@@ -367,7 +373,8 @@ def test_f32_lds_dma_kernel_selection(lib, shape, tile):
     assert info["workspace_bytes"] == 0
 
 
-@pytest.mark.parametrize("shape", [(4096, 4096, 64), (8192, 2048, 96), (1024, 1536, 48), (2048, 2048, 16)])
+@pytest.mark.parametrize("shape", [(4096, 4096, 64), (8192, 2048, 96), (1024, 1536, 48), (2048, 2048, 16),
+                                   (1000, 1000, 1000), (300, 1012, 60), (2100, 900, 36)])
 def test_f32_lds_dma_against_float64_brute_force(lib, shape, tune):
     # The LDS-DMA kernel sums each stage's 16 K values in a permuted order (lane half h takes K 8h + t
     # at step t); every element must still sit within the fp32 accumulation bound of an fp64
@@ -390,9 +397,11 @@ def test_f32_lds_dma_against_float64_brute_force(lib, shape, tune):
 
 @pytest.mark.parametrize("shape, tile", [((4096, 8192, 64), (256, 128)), ((8192, 4096, 40), (256, 128)),
                                          ((2048, 2048, 2048), (128, 128)), ((1024, 1536, 40), (128, 128)),
-                                         ((4096, 8192, 60), None), ((4096, 8000, 64), None)])
+                                         ((4096, 8192, 60), (256, 128)), ((4096, 8000, 64), (256, 128)),
+                                         ((4096, 8001, 64), None), ((4096, 8192, 61), None)])
 def test_f64_lds_dma_kernel_selection(lib, shape, tile):
-    # fp64: 256 x 128 tiles when they cover every CU, else 128 x 128; K in whole stages of 8.
+    # fp64: 256 x 128 tiles when they cover every CU, else 128 x 128, partial last tiles and a K off the
+    # 8-deep stage included; rows of A or B off 16 bytes keep the register-staged kernel.
     info = lib.gemm_info(capi.DT_FLOAT64, *shape)
     if tile is None:
         assert info["implementation"] == "gfx950_mfma_f64_16x16x4" and info["tile_m"] == 128
@@ -401,7 +410,8 @@ def test_f64_lds_dma_kernel_selection(lib, shape, tile):
         assert (info["tile_m"], info["tile_n"]) == tile
 
 
-@pytest.mark.parametrize("shape", [(4096, 8192, 40), (8192, 4096, 24), (1024, 1536, 40), (2048, 2048, 8)])
+@pytest.mark.parametrize("shape", [(4096, 8192, 40), (8192, 4096, 24), (1024, 1536, 40), (2048, 2048, 8),
+                                   (1000, 1000, 1002), (300, 1012, 62), (2100, 900, 36)])
 def test_f64_lds_dma_against_float64_brute_force(lib, shape, tune):
     # K permuted inside each stage (lane group g takes K 2g + t at step t); every element within the
     # fp64 accumulation bound of the brute force, and the staged kernel (forced) within the same bound.
@@ -555,7 +565,8 @@ def test_split_k_reduction_ignores_workspace_contents(lib, dtype, config, splits
     ops2 = rp.gemm_inputs(m2, n2, k2, dtype, seed=7)
     c2 = torch.empty((m2, n2), dtype=rp.gemm_output_dtype(dtype), device="cuda")
     assert lib.gemm_workspace_size(dt, m2, n2, k2) <= ws_bytes
-    lib.gemm(dt, ops2["a"].cuda().data_ptr(), ops2["b"].cuda().data_ptr(), c2.data_ptr(), m2, n2, k2,
+    a2, b2 = ops2["a"].cuda(), ops2["b"].cuda()   # held until the launch has run
+    lib.gemm(dt, a2.data_ptr(), b2.data_ptr(), c2.data_ptr(), m2, n2, k2,
              ops2["scale_a"], ops2["scale_b"], ws.data_ptr(), ws_bytes, stream)
     results.append(run(ws))
     for r in results:
@@ -630,7 +641,9 @@ def test_overrides_are_reported_and_the_environment_is_ignored(lib, tune, monkey
     ("float8_e4m3fn", (256, 256, 100), "gfx950_mfma_generic", "K is not a multiple of 16"),
     ("bfloat16", (256, 256, 100), "gfx950_mfma_generic", "K is not a multiple of 8"),
     ("float8_e4m3fn", (256, 256, 96), "gfx950_mfma32_lds_dma", ""),
-    ("float32", (300, 200, 64), "gfx950_mfma_f32_32x32x2", "M or N is not a multiple of 128"),
+    ("float32", (300, 201, 64), "gfx950_mfma_f32_32x32x2", "N is not a multiple of 4"),
+    ("float64", (300, 200, 63), "gfx950_mfma_f64_16x16x4", "K is not a multiple of 2"),
+    ("float32", (300, 200, 60), "gfx950_mfma_f32_32x32x2_lds_dma", ""),
     ("bfloat16", (256, 256, 256), "gfx950_mfma32_lds_dma", ""),
 ])
 def test_kernel_info_names_the_fallback(lib, dtype, shape, impl, reason):

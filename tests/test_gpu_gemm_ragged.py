@@ -169,3 +169,33 @@ def test_bounds_checked_kernel_forced(lib, tune, dtype, shape):
     tune(gemm_force_generic=1)
     info = run_checked(lib, dtype, *shape, seed=len(shape) + shape[0])
     assert info["implementation"] == GENERIC, info
+
+
+@pytest.mark.parametrize("dtype", ["float32", "float64"])
+@pytest.mark.parametrize("shape", [(1000, 1000, 1000), (300, 1012, 60), (2100, 900, 36), (257, 4100, 20),
+                                   (4100, 8000, 36)])
+def test_full_precision_ring_on_partial_tiles(lib, dtype, shape):
+    # fp32 / fp64 on the LDS-DMA rings with partial last tiles and a K off the stage: nothing written past
+    # C, every element of C written, sampled rows within the accumulation bound of an fp64 matmul.
+    m, n, k = shape
+    dt = capi.DTYPES[dtype]
+    info = lib.gemm_info(dt, m, n, k)
+    assert info["implementation"].endswith("_lds_dma"), info
+    print(f"[gemm-ragged] {dtype} {m}x{n}x{k}: {info['tile_m']}x{info['tile_n']}", flush=True)
+    ops = rp.gemm_inputs(m, n, k, dtype, seed=m + k)
+    tdt = torch.float32 if dtype == "float32" else torch.float64
+    flat = torch.full((m * n + GUARD,), float("nan"), dtype=tdt, device="cuda")
+    dc = flat[: m * n].view(m, n)
+    da, db = ops["a"].cuda(), ops["b"].cuda()   # held: their memory must outlive the launch
+    lib.gemm(dt, da.data_ptr(), db.data_ptr(), dc.data_ptr(), m, n, k, 1.0, 1.0, None, 0,
+             torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    assert torch.isnan(flat[m * n:]).all(), "the GEMM wrote past the end of C"
+    got_all = dc.cpu().double().numpy()
+    assert not np.isnan(got_all).any(), "C has unwritten (NaN-filled) elements"
+    rows = np.unique(np.concatenate([[0, m - 1], np.random.default_rng(k).choice(m, size=min(m, 62), replace=False)]))
+    a64, b64 = ops["a"].double().numpy()[rows], ops["b"].double().numpy()
+    ref = a64 @ b64
+    unit = 2.0**-24 if dtype == "float32" else 2 * 2.0**-53
+    bound = np.abs(ref) * unit + (k + 1) * unit * (np.abs(a64) @ np.abs(b64))
+    assert (np.abs(got_all[rows] - ref) <= bound + 1e-300).all()
