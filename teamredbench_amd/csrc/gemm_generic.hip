@@ -1,7 +1,7 @@
 // General-shape GEMM for gfx950: C = alpha * A * B (row-major) with fp32
 // MFMA accumulation, for any M, N, K >= 1. It takes the shapes the LDS-DMA
-// kernels cannot: B rows not on 16 bytes (N not a multiple of 8, of 16 for
-// fp8) or K not a multiple of 64 bytes. Every global access is bounds-checked.
+// kernels cannot: A or B rows not on 16 bytes (K or N not a multiple of 8, of
+// 16 for fp8). Every global access is bounds-checked.
 //
 // Block: 256 threads = 4 waves in a 2 x 2 grid; block tile 128 x 128; each
 // wave owns 64 x 64 of C as 2 x 2 fragments of 32 x 32
