@@ -12,6 +12,11 @@ if str(ROOT) not in sys.path:
     sys.path.insert(0, str(ROOT))
 
 
+def pytest_addoption(parser):
+    parser.addoption("--gemm-random-cases", type=int, default=20,
+                     help="seeded random GEMM shapes per input type in test_gpu_gemm_random.py (default 20)")
+
+
 def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs an MI355X (gfx950) GPU and the built libmi355bench.so")
 

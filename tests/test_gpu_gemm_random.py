@@ -31,7 +31,6 @@ from teamredbench_amd.native import capi
 
 pytestmark = pytest.mark.gpu
 
-CASES = 20
 IMPLEMENTATIONS = {"gfx950_gemv_stream", "gfx950_mfma16_lds_dma", "gfx950_mfma32_lds_dma", "gfx950_mfma_generic",
                    "gfx950_mfma_f32_32x32x2", "gfx950_mfma_f32_32x32x2_lds_dma", "gfx950_mfma_f64_16x16x4",
                    "gfx950_mfma_f64_16x16x4_lds_dma"}
@@ -65,8 +64,13 @@ def random_shape(dtype: str, case: int) -> tuple[int, int, int]:
     return max(m, 1), n, k
 
 
+def pytest_generate_tests(metafunc):
+    # 20 seeded cases per input type; `--gemm-random-cases N` runs N (a wider sweep of the same draws)
+    if "case" in metafunc.fixturenames:
+        metafunc.parametrize("case", range(metafunc.config.getoption("--gemm-random-cases")))
+
+
 @pytest.mark.parametrize("dtype", DTYPES)
-@pytest.mark.parametrize("case", range(CASES))
 def test_planned_gemm_on_random_shapes(lib, dtype, case):
     m, n, k = random_shape(dtype, case)
     dt = capi.DTYPES[dtype]
