@@ -95,7 +95,7 @@ gemm_generic_kernel(const unsigned char* __restrict__ A, const unsigned char* __
     const int64_t a_row = m0 + ar, b_col = n0 + bc;
 
     // One element of A or B (zero-extended), and 32 bytes of them packed in order.
-    auto elem = [](const unsigned char* p) -> unsigned __attribute__((always_inline)) {
+    auto elem = [](const unsigned char* p) __attribute__((always_inline)) -> unsigned {
         if constexpr (E == 1) return (unsigned)*p;
         else return (unsigned)*reinterpret_cast<const uint16_t*>(p);
     };
