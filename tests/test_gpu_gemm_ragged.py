@@ -201,23 +201,31 @@ def test_full_precision_ring_on_partial_tiles(lib, dtype, shape):
     assert (np.abs(got_all[rows] - ref) <= bound + 1e-300).all()
 
 
-def test_bounds_checked_kernel_beyond_32_bit_offsets(lib):
-    # B of 32768 x 65536 bf16 (4 GiB) is past the 32-bit buffer offsets of the pipelined kernels, so the
-    # bounds-checked kernel (64-bit indexing) takes it. A's rows are one-hot, each selecting a row of B
-    # spread over all of K (the last included), so C's rows must equal those B rows exactly.
+@pytest.mark.parametrize("dtype", ["bfloat16", "float8_e4m3fn"])
+def test_bounds_checked_kernel_beyond_32_bit_offsets(lib, dtype):
+    # B of 32768 x 65536 (4 GiB in bf16, 2^31 bytes in fp8) is past the 32-bit buffer offsets of the
+    # pipelined kernels, so the bounds-checked kernel (64-bit indexing) takes it. A's rows are one-hot, each
+    # selecting a row of B spread over all of K (the last included), so C's rows must equal those B rows
+    # exactly: every e4m3 value is a bf16 value. Values, not bits, are compared: a B element of -0 comes
+    # back as +0 from the accumulator.
     m, n, k = 64, 65536, 32768
-    info = lib.gemm_info(capi.DT_BFLOAT16, m, n, k)
+    dt, tdt = capi.DTYPES[dtype], getattr(torch, dtype)
+    info = lib.gemm_info(dt, m, n, k)
     assert info["implementation"] == GENERIC and "32-bit" in info["fallback"], info
     gen = torch.Generator(device="cuda").manual_seed(3)
-    b = torch.randn(k, n, device="cuda", dtype=torch.bfloat16, generator=gen)
+    b = torch.randn(k, n, device="cuda", dtype=torch.bfloat16, generator=gen).to(tdt)
     sel = torch.tensor([k - 1] + [(i * 2654435761) % k for i in range(1, m)], device="cuda")
-    a = torch.zeros(m, k, device="cuda", dtype=torch.bfloat16)
-    a[torch.arange(m, device="cuda"), sel] = 1.0
-    flat = torch.full((m * n + GUARD,), float("nan"), dtype=torch.bfloat16, device="cuda")
+    a16 = torch.zeros(m, k, device="cuda", dtype=torch.bfloat16)
+    a16[torch.arange(m, device="cuda"), sel] = 1.0
+    a = a16.to(tdt)
+    out = rp.gemm_output_dtype(dtype)
+    flat = torch.full((m * n + GUARD,), float("nan"), dtype=out, device="cuda")
     c = flat[: m * n].view(m, n)
-    print(f"[gemm-ragged] bf16 {m}x{n}x{k} (B 4 GiB): {info['implementation']}", flush=True)
-    lib.gemm(capi.DT_BFLOAT16, a.data_ptr(), b.data_ptr(), c.data_ptr(), m, n, k, 1.0, 1.0, None, 0,
+    print(f"[gemm-ragged] {dtype} {m}x{n}x{k} (B {k * n * b.element_size() >> 30} GiB): "
+          f"{info['implementation']}", flush=True)
+    lib.gemm(dt, a.data_ptr(), b.data_ptr(), c.data_ptr(), m, n, k, 1.0, 1.0, None, 0,
              torch.cuda.current_stream().cuda_stream)
     torch.cuda.synchronize()
     assert torch.isnan(flat[m * n:].float()).all(), "the GEMM wrote past the end of C"
-    assert torch.equal(c.view(torch.int16), b[sel].view(torch.int16))
+    picked = b.view(torch.uint8 if b.element_size() == 1 else torch.int16)[sel].view(tdt)  # gather as integers
+    assert torch.equal(c, picked.to(out))
