@@ -201,31 +201,40 @@ def test_full_precision_ring_on_partial_tiles(lib, dtype, shape):
     assert (np.abs(got_all[rows] - ref) <= bound + 1e-300).all()
 
 
-@pytest.mark.parametrize("dtype", ["bfloat16", "float8_e4m3fn"])
-def test_bounds_checked_kernel_beyond_32_bit_offsets(lib, dtype):
-    # B of 32768 x 65536 (4 GiB in bf16, 2^31 bytes in fp8) is past the 32-bit buffer offsets of the
-    # pipelined kernels, so the bounds-checked kernel (64-bit indexing) takes it. A's rows are one-hot, each
-    # selecting a row of B spread over all of K (the last included), so C's rows must equal those B rows
-    # exactly: every e4m3 value is a bf16 value. Values, not bits, are compared: a B element of -0 comes
-    # back as +0 from the accumulator.
-    m, n, k = 64, 65536, 32768
+# Shapes whose B passes 2^31 bytes, with the kernel each must run on.
+BEYOND_32_BIT = [
+    ("bfloat16", 65536, GENERIC),                     # B 4 GiB
+    ("float8_e4m3fn", 65536, GENERIC),                # B 2 GiB
+    ("float32", 16384, "gfx950_mfma_f32_32x32x2"),    # B 2 GiB, register-staged fp32 kernel
+    ("float64", 8192, "gfx950_mfma_f64_16x16x4"),     # B 2 GiB, register-staged fp64 kernel
+]
+
+
+@pytest.mark.parametrize("dtype,n,kernel", BEYOND_32_BIT)
+def test_kernels_with_64_bit_offsets_beyond_32_bit_buffers(lib, dtype, n, kernel):
+    # B of 32768 x n is past the 32-bit buffer offsets of the LDS-DMA kernels, so a kernel that indexes
+    # with 64-bit offsets takes it. A's rows are one-hot, each selecting a row of B spread over all of K
+    # (the last included), so C's rows must equal those B rows exactly: every e4m3 value is a bf16 value.
+    # Values, not bits, are compared: a B element of -0 comes back as +0 from the accumulator.
+    m, k = 64, 32768
     dt, tdt = capi.DTYPES[dtype], getattr(torch, dtype)
     info = lib.gemm_info(dt, m, n, k)
-    assert info["implementation"] == GENERIC and "32-bit" in info["fallback"], info
+    assert info["implementation"] == kernel and "32-bit" in info["fallback"], info
     gen = torch.Generator(device="cuda").manual_seed(3)
-    b = torch.randn(k, n, device="cuda", dtype=torch.bfloat16, generator=gen).to(tdt)
+    wide = tdt if tdt in (torch.float32, torch.float64) else torch.bfloat16
+    b = torch.randn(k, n, device="cuda", dtype=wide, generator=gen).to(tdt)
     sel = torch.tensor([k - 1] + [(i * 2654435761) % k for i in range(1, m)], device="cuda")
-    a16 = torch.zeros(m, k, device="cuda", dtype=torch.bfloat16)
-    a16[torch.arange(m, device="cuda"), sel] = 1.0
-    a = a16.to(tdt)
+    one_hot = torch.zeros(m, k, device="cuda", dtype=wide)
+    one_hot[torch.arange(m, device="cuda"), sel] = 1.0
+    a = one_hot.to(tdt)
     out = rp.gemm_output_dtype(dtype)
     flat = torch.full((m * n + GUARD,), float("nan"), dtype=out, device="cuda")
     c = flat[: m * n].view(m, n)
-    print(f"[gemm-ragged] {dtype} {m}x{n}x{k} (B {k * n * b.element_size() >> 30} GiB): "
-          f"{info['implementation']}", flush=True)
+    print(f"[gemm-ragged] {dtype} {m}x{n}x{k} (B {k * n * b.element_size() >> 30} GiB): {kernel}", flush=True)
     lib.gemm(dt, a.data_ptr(), b.data_ptr(), c.data_ptr(), m, n, k, 1.0, 1.0, None, 0,
              torch.cuda.current_stream().cuda_stream)
     torch.cuda.synchronize()
     assert torch.isnan(flat[m * n:].float()).all(), "the GEMM wrote past the end of C"
-    picked = b.view(torch.uint8 if b.element_size() == 1 else torch.int16)[sel].view(tdt)  # gather as integers
+    as_int = {1: torch.uint8, 2: torch.int16, 4: torch.int32, 8: torch.int64}[b.element_size()]
+    picked = b.view(as_int)[sel].view(tdt)   # gathered as integers: fp8 has no index kernels
     assert torch.equal(c, picked.to(out))
