@@ -165,3 +165,29 @@ def test_nontemporal_hint_follows_the_pass_size(lib, mode, dtype, n, nontemporal
     assert info["nontemporal"] is nontemporal, info
     with lib.tuned(stream_nontemporal=0 if nontemporal else 1):    # the knob still overrides it
         assert lib.stream_info(capi.OPS[mode], capi.DTYPES[dtype], n)["nontemporal"] is not nontemporal
+
+
+def test_triad_and_copy_past_2_31_elements(lib):
+    # n = 2^31 + 13 bf16 elements (4 GiB per array): element indexes and byte offsets past 32 bits. Checked
+    # on the device in slices: the triad against fp32 fma then RNE to bf16 (for bf16 inputs b + 3c is exact
+    # in fp64, so rounding it to fp32 is the fma), the copy bit for bit; a guard after dst stays untouched.
+    n, guard = (1 << 31) + 13, 4096
+    print(f"[stream] triad/copy bfloat16 n=2^31+13", flush=True)
+    gen = torch.Generator(device="cuda").manual_seed(11)
+    b = torch.rand(n, device="cuda", dtype=torch.bfloat16, generator=gen) * 2 - 1
+    c = torch.rand(n, device="cuda", dtype=torch.bfloat16, generator=gen) * 2 - 1
+    flat = torch.full((n + guard,), 7, dtype=torch.bfloat16, device="cuda")
+    dst = flat[:n]
+    stream = torch.cuda.current_stream().cuda_stream
+    step = 1 << 28
+    for mode in ("triad", "copy"):
+        lib.stream(capi.OPS[mode], capi.DTYPES["bfloat16"], dst.data_ptr(), b.data_ptr(),
+                   c.data_ptr() if mode == "triad" else None, n, 3.0, 0, stream)
+        torch.cuda.synchronize()
+        assert (flat[n:] == 7).all(), f"{mode} wrote past the end of dst"
+        for i in range(0, n, step):
+            if mode == "triad":
+                want = (b[i:i + step].double() + 3.0 * c[i:i + step].double()).float().bfloat16()
+            else:
+                want = b[i:i + step]
+            assert torch.equal(dst[i:i + step].view(torch.int16), want.view(torch.int16)), (mode, i)
