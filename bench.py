@@ -12,8 +12,12 @@ in HBM. The printed JSON line carries:
                        recorded on the launch stream, against 8000 GB/s;
                        `traffic` is the HBM bytes per launch from the committed
                        rocprofv3 FETCH_SIZE/WRITE_SIZE summary, when present;
+                       `launch_us` the min / median / max of the per-launch
+                       event durations and `clock` the shader clock each XCD
+                       ran at over the timed loop (clock stamps on its stream);
   gemm                 bf16 and fp8 e4m3 GEMM TFLOPS and MFU at 8192^3
-                       (event-timed, same library), with a sampled parity check,
+                       (event-timed per launch, same library, with the same
+                       `launch_us` spread and `clock`), a sampled parity check,
                        and each one's CPU baseline: torch.mm on CPU tensors over
                        a 512-row slab of the same problem (bf16 operands for
                        bf16; for fp8, whose torch.mm has no CPU kernel, the
@@ -40,6 +44,7 @@ ROOT = Path(__file__).resolve().parent
 if str(ROOT) not in sys.path:
     sys.path.insert(0, str(ROOT))
 
+
 HBM_PEAK_GBPS = 8000.0
 MFMA_PEAK_TFLOPS = {"bfloat16": 2500.0, "float16": 2500.0, "float8_e4m3fn": 5000.0}
 GEMM_WARMUP_S = 0.25
@@ -49,6 +54,15 @@ TRAFFIC_SUMMARY = ROOT / "profiles" / "stream_triad_f32_2p28_traffic.txt"
 
 def _log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def launch_spread(seconds: list[float]) -> dict:
+    """Min / median / max / mean of per-launch HIP-event durations, in microseconds."""
+    ordered = sorted(seconds)
+    mid = len(ordered) // 2
+    median = ordered[mid] if len(ordered) % 2 else 0.5 * (ordered[mid - 1] + ordered[mid])
+    return {"min": round(ordered[0] * 1e6, 2), "median": round(median * 1e6, 2), "max": round(ordered[-1] * 1e6, 2),
+            "mean": round(sum(ordered) / len(ordered) * 1e6, 2), "launches": len(ordered)}
 
 
 def read_traffic() -> dict | None:
@@ -66,6 +80,8 @@ def read_traffic() -> dict | None:
 
 
 def bench_triad(torch, lib, capi, steps: int, warmup: int) -> dict:
+    from teamredbench_amd.profiling.clock import ClockWindow
+
     n = TRIAD_ELEMENTS
     dev = torch.device("cuda:0")
     gen = torch.Generator(device=dev)
@@ -82,16 +98,23 @@ def bench_triad(torch, lib, capi, steps: int, warmup: int) -> dict:
     for _ in range(warmup):
         step()
     torch.cuda.synchronize()
-    start_ev = torch.cuda.Event(enable_timing=True)
-    stop_ev = torch.cuda.Event(enable_timing=True)
+    # One event before the first launch and one after each: launch i spans events i .. i + 1, and the
+    # first and last bracket the whole loop, which the wall clock brackets too.
+    # The clock stamps bracket the loop on its stream (two one-wave kernels of a few microseconds, the
+    # second inside the wall-clock window).
+    events = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
+    clock = ClockWindow(torch, lib, handle)
+    clock.start()
     t0 = time.perf_counter()
-    start_ev.record(stream)
-    for _ in range(steps):
+    events[0].record(stream)
+    for i in range(steps):
         step()
-    stop_ev.record(stream)
+        events[i + 1].record(stream)
+    clock.stop()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    event_s = start_ev.elapsed_time(stop_ev) / 1000.0 / steps
+    event_s = events[0].elapsed_time(events[-1]) / 1000.0 / steps
+    per_launch = [events[i].elapsed_time(events[i + 1]) / 1000.0 for i in range(steps)]
 
     # in-run parity against the torch GPU op (1 ulp bound of the stream configuration)
     from teamredbench_amd.parity import stream_parity
@@ -103,6 +126,8 @@ def bench_triad(torch, lib, capi, steps: int, warmup: int) -> dict:
     return {
         "wall_s_per_step": wall / steps,
         "event_s_per_launch": event_s,
+        "launch_us": launch_spread(per_launch),
+        "clock": clock.summary(),
         "moved_bytes": moved,
         "parity": parity,
         "info": lib.stream_info(capi.OP_TRIAD, capi.DT_FLOAT32, n),
@@ -111,6 +136,7 @@ def bench_triad(torch, lib, capi, steps: int, warmup: int) -> dict:
 
 def bench_gemm(torch, lib, capi, dtype: str, size: int, warmup: int, iterations: int) -> dict:
     from teamredbench_amd.parity import gemm_parity
+    from teamredbench_amd.profiling.clock import ClockWindow
     from teamredbench_amd.utils import seeded_gemm_operands
 
     dev = torch.device("cuda:0")
@@ -127,8 +153,20 @@ def bench_gemm(torch, lib, capi, dtype: str, size: int, warmup: int, iterations:
     est = lib.time_gemm(dt, a.data_ptr(), b.data_ptr(), c.data_ptr(), m, n, k, sa, sb, ws.data_ptr(), ws_bytes,
                         0, 2, handle)
     warmup = max(warmup, int(GEMM_WARMUP_S / est) + 1)
-    secs = lib.time_gemm(dt, a.data_ptr(), b.data_ptr(), c.data_ptr(), m, n, k, sa, sb, ws.data_ptr(), ws_bytes,
-                         warmup, iterations, handle)
+    lib.time_gemm(dt, a.data_ptr(), b.data_ptr(), c.data_ptr(), m, n, k, sa, sb, ws.data_ptr(), ws_bytes,
+                  warmup, 1, handle)
+    stream = torch.cuda.current_stream(dev)
+    events = [torch.cuda.Event(enable_timing=True) for _ in range(iterations + 1)]
+    clock = ClockWindow(torch, lib, handle)
+    clock.start()
+    events[0].record(stream)
+    for i in range(iterations):
+        lib.gemm(dt, a.data_ptr(), b.data_ptr(), c.data_ptr(), m, n, k, sa, sb, ws.data_ptr(), ws_bytes, handle)
+        events[i + 1].record(stream)
+    clock.stop()
+    torch.cuda.synchronize()
+    secs = events[0].elapsed_time(events[-1]) / 1000.0 / iterations
+    per_launch = [events[i].elapsed_time(events[i + 1]) / 1000.0 for i in range(iterations)]
     rows = torch.randperm(m, generator=torch.Generator().manual_seed(0))[:256].to(dev)
     ref = (a[rows].float() * sa) @ (b.float() * sb)
     parity = gemm_parity(torch, dtype, c[rows].float(), ref)
@@ -140,6 +178,8 @@ def bench_gemm(torch, lib, capi, dtype: str, size: int, warmup: int, iterations:
     return {
         "shape": [m, n, k],
         "latency_us": secs * 1e6,
+        "launch_us": launch_spread(per_launch),
+        "clock": clock.summary(),
         "achieved_tflops": tflops,
         "mfu_pct": 100.0 * tflops / MFMA_PEAK_TFLOPS[dtype],
         "parity": {**parity, "rows_checked": 256},
@@ -339,6 +379,8 @@ def main() -> int:
             "traffic": traffic["bytes"] if traffic else None,
             "algorithmic_bytes": triad["moved_bytes"],
             "kernel": triad["info"].get("implementation"),
+            "launch_us": triad["launch_us"],
+            "clock": triad["clock"],
         },
         "parity": triad["parity"],
         "kernel_info": triad["info"],

@@ -224,6 +224,27 @@ int mb_set_tuning(int knob, int64_t value);
 /* The value `knob` holds (-1 = the library's choice); -1 for an unknown knob. */
 int64_t mb_get_tuning(int knob);
 
+/*
+ * Clock stamps. No counterpart in the reference: a measurement aid that
+ * tells at which clock a timed region ran (the part runs MFMA-heavy kernels
+ * under its power limit, well below the clock its peak figures assume).
+ * Enqueues on `stream` one kernel of MB_CLOCK_BLOCKS one-wave blocks, enough
+ * for the dispatcher to place blocks on every CU; block b writes
+ *   out[4b]     its CU's shader-clock counter (s_memtime),
+ *   out[4b + 1] the constant MB_CLOCK_REALTIME_HZ counter (s_memrealtime),
+ *   out[4b + 2] the id of the XCD it ran on (XCC_ID),
+ *   out[4b + 3] its wave's HW_ID register (bits 15:8: CU, shader array and
+ *               shader engine within the XCD).
+ * `out` is device memory for 4 * MB_CLOCK_BLOCKS uint64_t. The shader-clock
+ * counters of different CUs are not synchronised, so two stamps on the
+ * stream around a region are paired CU by CU: each CU seen in both gives its
+ * XCD's mean shader clock over the region,
+ * (memtime_1 - memtime_0) / (memrealtime_1 - memrealtime_0) * MB_CLOCK_REALTIME_HZ.
+ */
+#define MB_CLOCK_BLOCKS 1024
+#define MB_CLOCK_REALTIME_HZ 100000000
+int mb_clock_stamp(uint64_t* out, void* stream);
+
 /* Description of the last failure on the calling thread ("" if none). */
 const char* mb_last_error(void);
 

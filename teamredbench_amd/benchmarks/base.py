@@ -22,7 +22,6 @@ from __future__ import annotations
 
 from abc import ABC, abstractmethod
 from dataclasses import dataclass, field
-import json
 from pathlib import Path
 from typing import Any, Callable
 
@@ -83,14 +82,14 @@ class BenchmarkRecord:
         )
 
     def to_row(self) -> dict[str, Any]:
-        """The flat CSV row: identity columns, then metric_* / raw_* / meta_* in key order.
-        Nested values (a parity dict, a shape list) are written as JSON text."""
+        """The flat CSV row: identity columns, then metric_* / raw_* / meta_* in key order. Values go to
+        the CSV writer as they are, so a nested one (a parity dict, a shape list) is written as its Python
+        text, str(value), the form the reference's CSV holds (src/teamredbench/io.py:25-39)."""
         row: dict[str, Any] = {"benchmark": self.benchmark, "case": self.case, "dtype": self.dtype,
                                "status": self.status, "error": self.error or ""}
         for prefix, values in (("metric", self.metrics), ("raw", self.raw_metrics), ("meta", self.metadata)):
             for key in sorted(values):
-                value = values[key]
-                row[f"{prefix}_{key}"] = json.dumps(value) if isinstance(value, (dict, list, tuple)) else value
+                row[f"{prefix}_{key}"] = values[key]
         return row
 
 

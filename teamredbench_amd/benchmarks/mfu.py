@@ -8,12 +8,13 @@ API and record shape follow src/teamredbench/benchmarks/mfu.py:
           warmup_seconds (default 0: untimed warmup lasts at least this
           long, more launches than `warmup` if need be -- the part leaves
           its low-power clock state only after tens of ms of MFMA work),
-          operand_sets ("auto", or a count: the native timed loop cycles
-          through that many copies of A, B and C; "auto" takes enough
-          copies to exceed three times the 256 MB Infinity Cache for a
-          memory-bound shape -- arithmetic intensity below the dtype's
-          ridge point, peak_tops / peak HBM bandwidth -- whose operands would
-          otherwise stay cache-resident between launches, and 1 otherwise)
+          operand_sets ("auto", or a count: the timed loop, native and torch
+          alike, cycles through that many copies of A, B and C; "auto" takes
+          enough copies to span three times the 256 MB Infinity Cache (at
+          most 1024) for a memory-bound shape -- arithmetic intensity below
+          the dtype's ridge point, peak_tops / peak HBM bandwidth -- whose
+          operands would otherwise stay cache-resident between launches, and
+          1 otherwise; 1 times a single set, as the reference does)
   record: case "gemm_<m>x<n>x<k>"; raw_metrics elapsed_s / achieved_ops
           (= matmul_ops_factor * m * n * k) / peak_tops, plus gemm_bytes
           ((mk + kn) * in_bytes + mn * out_bytes) for the effective-GB/s metric.
@@ -48,6 +49,10 @@ DEFAULT_SHAPES = [
 ]
 
 INFINITY_CACHE_BYTES = 256 * 1024 * 1024
+# Bytes the cycled operand sets of a memory-bound shape span (three times the Infinity Cache), and the
+# most sets "auto" takes to get there.
+OPERAND_FOOTPRINT_TARGET = 3 * INFINITY_CACHE_BYTES
+MAX_OPERAND_SETS = 1024
 
 
 def gemm_bytes(m: int, n: int, k: int, in_bytes: int, out_bytes: int) -> int:
@@ -147,18 +152,34 @@ class MfuBenchmark(Benchmark):
                 torch.cuda.empty_cache()
         return records
 
-    def _operand_sets(self, spec, m: int, n: int, k: int, out_bytes: int, peak_tops: float | None) -> int:
+    def _operand_sets(self, spec, m: int, n: int, k: int, out_bytes: int,
+                      peak_tops: float | None) -> tuple[int, dict[str, Any]]:
+        """(operand sets to cycle through, metadata describing them).
+
+        One set is A, B and C. ``operand_sets: auto`` takes one set for a compute-bound shape (arithmetic
+        intensity at or above the dtype's ridge point, peak_tops / peak HBM bandwidth) or one whose set
+        already spans OPERAND_FOOTPRINT_TARGET, else enough sets to span that target (at most
+        MAX_OPERAND_SETS); an integer takes that many. The metadata gives the sets' total footprint,
+        ``cache_resident_b`` (true when that footprint fits the Infinity Cache, so the operands are re-read
+        from the cache rather than HBM) and, when ``auto`` stopped at MAX_OPERAND_SETS short of the target,
+        ``operand_footprint_short_of_target``."""
+        per_set = gemm_bytes(m, n, k, spec.bytes_per_element, out_bytes)
         requested = self.params.get("operand_sets", "auto")
         if requested != "auto":
-            return max(1, int(requested))
-        operand_bytes = (m * k + k * n) * spec.bytes_per_element
-        hbm = self.context.hardware_profile.peak_hbm_bandwidth_gbps
-        if not peak_tops or not hbm or operand_bytes > INFINITY_CACHE_BYTES:
-            return 1
-        intensity = spec.matmul_ops_factor * m * n * k / gemm_bytes(m, n, k, spec.bytes_per_element, out_bytes)
-        if intensity >= peak_tops * 1e12 / (hbm * 1e9):
-            return 1    # compute-bound: where the operands sit does not set the time
-        return min(64, max(3, -(-3 * INFINITY_CACHE_BYTES // operand_bytes)))
+            sets = max(1, int(requested))
+        else:
+            sets = 1
+            hbm = self.context.hardware_profile.peak_hbm_bandwidth_gbps
+            if peak_tops and hbm and per_set < OPERAND_FOOTPRINT_TARGET:
+                intensity = spec.matmul_ops_factor * m * n * k / per_set
+                if intensity < peak_tops * 1e12 / (hbm * 1e9):
+                    sets = min(MAX_OPERAND_SETS, -(-OPERAND_FOOTPRINT_TARGET // per_set))
+        footprint = sets * per_set
+        info: dict[str, Any] = {"operand_sets": sets, "operand_footprint_bytes": footprint,
+                                "cache_resident_b": footprint <= INFINITY_CACHE_BYTES}
+        if requested == "auto" and sets > 1 and footprint < OPERAND_FOOTPRINT_TARGET:
+            info["operand_footprint_short_of_target"] = True
+        return sets, info
 
     def _capi_case(self, lib, torch, spec, peak_tops, m, n, k, case, meta, warmup, iterations, seed, verify,
                    verify_rows) -> BenchmarkRecord:
@@ -167,7 +188,7 @@ class MfuBenchmark(Benchmark):
         out_dtype = getattr(torch, capi.GEMM_OUTPUT_DTYPES[spec.name])
         c = torch.empty((m, n), device=device, dtype=out_dtype)
         dt = capi.DTYPES[spec.name]
-        sets = self._operand_sets(spec, m, n, k, c.element_size(), peak_tops)
+        sets, set_info = self._operand_sets(spec, m, n, k, c.element_size(), peak_tops)
         ws_bytes = lib.gemm_workspace_size(dt, m, n, k)
         ws = torch.empty(ws_bytes, device=device, dtype=torch.uint8) if ws_bytes else None
         stream = torch.cuda.current_stream(device).cuda_stream
@@ -189,13 +210,11 @@ class MfuBenchmark(Benchmark):
         else:
             elapsed = lib.time_gemm(dt, a.data_ptr(), b.data_ptr(), c.data_ptr(), m, n, k, sa, sb, ws_ptr, ws_bytes,
                                     warmup, iterations, stream)
-        meta = {**meta, **lib.gemm_info(dt, m, n, k), "operand_sets": sets}
+        meta = {**meta, **lib.gemm_info(dt, m, n, k), **set_info}
         if spec.name in capi.FP8_DTYPES:
             meta["scale_a"], meta["scale_b"] = sa, sb
         in_bytes = spec.bytes_per_element
         moved = gemm_bytes(m, n, k, in_bytes, c.element_size())
-        # operands re-read from the Infinity Cache rather than HBM: one set that fits it
-        meta["cache_resident_b"] = sets == 1 and k * n * in_bytes <= INFINITY_CACHE_BYTES
         if verify:
             rows = min(m, verify_rows)
             if spec.name == "float64":
@@ -219,16 +238,31 @@ class MfuBenchmark(Benchmark):
     # torch.mm does not take, goes through torch._scaled_mm with the same
     # per-tensor scales and bf16 output; that routine requires B column-major,
     # so B is laid out so once, outside the timed region (recorded as b_layout).
-    def _torch_gemm(self, torch, spec, a, b, sa, sb, out):
-        """(callable that runs one GEMM, metadata naming the torch routine)."""
+    def _torch_gemm(self, torch, spec, a, b, sa, sb, out, sets: int = 1):
+        """(callable that runs one GEMM, metadata naming the torch routine). With `sets` > 1 the callable
+        cycles through that many copies of A, B and C, one per call, as the native timed loop does."""
+        copies = [(a, b, out)] + [(a.clone(), b.clone(), torch.empty_like(out)) for _ in range(sets - 1)]
+        turn = [0]
+
+        def next_set():
+            i = turn[0]
+            turn[0] = (i + 1) % sets
+            return copies[i]
+
         if spec.name in capi.FP8_DTYPES:
-            b_cols = b.t().contiguous().t()
+            copies = [(x, y.t().contiguous().t(), z) for x, y, z in copies]
             scale_a = torch.tensor(sa, dtype=torch.float32, device=a.device)
             scale_b = torch.tensor(sb, dtype=torch.float32, device=a.device)
-            run = lambda: torch._scaled_mm(a, b_cols, scale_a=scale_a, scale_b=scale_b,  # noqa: E731
-                                           out_dtype=torch.bfloat16)
-            return run, {"torch_op": "_scaled_mm", "b_layout": "column_major"}
-        return (lambda: torch.mm(a, b, out=out)), {"torch_op": "mm", "b_layout": "row_major"}
+
+            def run_fp8():
+                x, y, _ = next_set()
+                return torch._scaled_mm(x, y, scale_a=scale_a, scale_b=scale_b, out_dtype=torch.bfloat16)
+            return run_fp8, {"torch_op": "_scaled_mm", "b_layout": "column_major"}
+
+        def run():
+            x, y, z = next_set()
+            return torch.mm(x, y, out=z)
+        return run, {"torch_op": "mm", "b_layout": "row_major"}
 
     def _run_torch(self) -> list[BenchmarkRecord]:
         torch = self.context.torch_module
@@ -253,14 +287,16 @@ class MfuBenchmark(Benchmark):
                     a, b, sa, sb = seeded_gemm_operands(torch, m, n, k, spec.name, self.device, seed)
                     out_dtype = getattr(torch, capi.GEMM_OUTPUT_DTYPES.get(spec.name, spec.torch_attr))
                     out = torch.empty((m, n), device=self.device, dtype=out_dtype)
-                    gemm, routine = self._torch_gemm(torch, spec, a, b, sa, sb, out)
+                    sets, set_info = self._operand_sets(spec, m, n, k, out.element_size(), peak_tops)
+                    gemm, routine = self._torch_gemm(torch, spec, a, b, sa, sb, out, sets)
                     elapsed = timed_iterations(gemm, torch_module=torch, warmup=warmup, iterations=iterations)
+                    del gemm
                 except Exception as exc:  # noqa: BLE001 -- a dtype torch cannot multiply skips this case only
                     records.append(self.skip(case=case, dtype=spec.name, error=str(exc), metadata=meta))
                     continue
                 finally:
                     torch.cuda.empty_cache()
-                meta.update(routine, timing="wall_clock")
+                meta.update(routine, timing="wall_clock", **set_info)
                 records.append(self.measured(case=case, dtype=spec.name, metadata=meta, raw_metrics={
                     "elapsed_s": elapsed, "achieved_ops": spec.matmul_ops_factor * m * n * k, "peak_tops": peak_tops,
                     "gemm_bytes": gemm_bytes(m, n, k, spec.bytes_per_element, out.element_size())}))

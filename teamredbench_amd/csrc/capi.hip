@@ -278,6 +278,40 @@ int64_t mb_get_tuning(int knob) { return tuning(knob); }
 
 const char* mb_last_error(void) { return g_last_error.c_str(); }
 
+namespace {
+
+// One stamp per block from its first lane: the CU's shader-clock counter, the
+// constant-rate counter, the XCD id (hardware register XCC_ID, bits 3:0) and
+// the wave's HW_ID register, which names its CU within the XCD.
+__global__ void __launch_bounds__(64) clock_stamp_kernel(uint64_t* out) {
+    if (threadIdx.x != 0) return;
+    unsigned xcc, hw;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_HW_ID)" : "=s"(hw));
+    const uint64_t shader = __builtin_amdgcn_s_memtime();
+    const uint64_t real = __builtin_amdgcn_s_memrealtime();
+    out[4 * blockIdx.x] = shader;
+    out[4 * blockIdx.x + 1] = real;
+    out[4 * blockIdx.x + 2] = xcc & 0xFu;
+    out[4 * blockIdx.x + 3] = hw;
+}
+
+}  // namespace
+
+int mb_clock_stamp(uint64_t* out, void* stream) {
+    clear_error();
+    if (out == nullptr) {
+        set_error("mb_clock_stamp: null output pointer");
+        return MB_ERR_INVALID_ARG;
+    }
+    const DeviceProps* props = nullptr;
+    int rc = device_for_launch(&props);
+    if (rc != MB_OK) return rc;
+    hipLaunchKernelGGL(clock_stamp_kernel, dim3(MB_CLOCK_BLOCKS), dim3(64), 0, static_cast<hipStream_t>(stream), out);
+    MB_HIP_TRY(hipGetLastError());
+    return MB_OK;
+}
+
 int mb_stream(int op, int dtype, void* dst, const void* b, const void* c, uint64_t n, double s,
               int blocks_per_cu, void* stream) {
     clear_error();

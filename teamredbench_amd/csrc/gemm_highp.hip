@@ -553,6 +553,12 @@ int highp_dma_config(bool f64, int64_t M, int64_t N, int64_t K, int cus, const c
         *why = "operand offsets exceed 32-bit buffer addressing (K*N or 256*K bytes >= 2 GiB)";
         return 0;
     }
+    // The LDS-DMA kernels take M and N as int (row and column guards); the
+    // register-staged kernel indexes with int64.
+    if (M >= (int64_t(1) << 31) || N >= (int64_t(1) << 31)) {
+        *why = "M or N >= 2^31 exceeds the 32-bit row and column indexes of the LDS-DMA kernels";
+        return 0;
+    }
     const int64_t bm = 256, bn = f64 ? 128 : 256;
     auto tiles = [&](int64_t tm, int64_t tn) { return ((M + tm - 1) / tm) * ((N + tn - 1) / tn); };
     const bool fits_large = tiles(bm, bn) >= cus && tiles(bm, bn) <= INT32_MAX;

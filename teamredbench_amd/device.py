@@ -88,6 +88,70 @@ def detect_device(torch_module: Any, device_id: int = 0) -> DeviceInfo | None:
     return DeviceInfo(index=device_id, name=str(props.name), **found)
 
 
+# Peak engine clock (MHz) -> SKU, for gfx950 parts whose marketing name the platform does not report
+# (the device name comes from libdrm's amdgpu.ids table, which a container may lack). MI355X and MI350X
+# are both gfx950 with 256 CUs; their published peak engine clocks differ.
+_GFX950_SKU_BY_MAX_CLOCK = {2400: "AMD Instinct MI355X", 2200: "AMD Instinct MI350X"}
+
+
+def _amdsmi_names(torch_module: Any, device_id: int) -> list[str]:
+    """The board's FRU product name, the ASIC's market name and, for gfx950, the SKU its peak engine clock
+    identifies, as amdsmi reports them for the device with torch device `device_id`'s PCI address."""
+    try:
+        import amdsmi
+    except Exception:  # noqa: BLE001 -- absent or broken: no names
+        return []
+    names: list[str] = []
+    try:
+        amdsmi.amdsmi_init()
+    except Exception:  # noqa: BLE001
+        return []
+    try:
+        props = torch_module.cuda.get_device_properties(device_id)
+        bdf = f"{props.pci_domain_id:04x}:{props.pci_bus_id:02x}:{props.pci_device_id:02x}.0"
+        handles = amdsmi.amdsmi_get_processor_handles()
+        handle = next((h for h in handles if str(amdsmi.amdsmi_get_gpu_device_bdf(h)).lower() == bdf), None)
+        if handle is None and len(handles) == 1:
+            handle = handles[0]
+        if handle is None:
+            return []
+        for getter, key in ((amdsmi.amdsmi_get_gpu_board_info, "product_name"),
+                            (amdsmi.amdsmi_get_gpu_asic_info, "market_name")):
+            try:
+                value = getter(handle).get(key)
+            except Exception:  # noqa: BLE001
+                continue
+            if isinstance(value, str) and value.strip() and value != "N/A":
+                names.append(value.strip())
+        arch = str(getattr(props, "gcnArchName", "") or "")
+        if arch.startswith("gfx950"):
+            try:
+                top = int(amdsmi.amdsmi_get_clock_info(handle, amdsmi.AmdSmiClkType.GFX)["max_clk"])
+            except Exception:  # noqa: BLE001
+                top = None
+            if top in _GFX950_SKU_BY_MAX_CLOCK:
+                names.append(f"{_GFX950_SKU_BY_MAX_CLOCK[top]} (gfx950, peak engine clock {top} MHz)")
+    except Exception:  # noqa: BLE001
+        return names
+    finally:
+        try:
+            amdsmi.amdsmi_shut_down()
+        except Exception:  # noqa: BLE001
+            pass
+    return names
+
+
+def product_names(torch_module: Any, device_id: int = 0) -> list[str]:
+    """Other names of the device than torch's: amdsmi's (see _amdsmi_names) and the product lines
+    ``rocm-smi --showproductname`` prints. Used to find the SKU when torch's name does not carry it."""
+    names = _amdsmi_names(torch_module, device_id)
+    text = _run_command(["rocm-smi", "--showproductname"])
+    if text:
+        names += [line.split(":", 2)[-1].strip() for line in text.splitlines()
+                  if "card series" in line.lower() or "card sku" in line.lower() or "card model" in line.lower()]
+    return [n for n in names if n]
+
+
 def _run_command(command: list[str]) -> str | None:
     """stdout of a tool, stripped; None when the tool is absent, fails or prints nothing."""
     if shutil.which(command[0]) is None:

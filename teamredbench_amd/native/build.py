@@ -86,6 +86,7 @@ def _compile(hipcc: str, src: Path, obj: Path) -> tuple[Path, int, str]:
 def build(verbose: bool = False, jobs: int | None = None) -> Path:
     """Compile every csrc/*.hip for gfx950 and link libmi355bench.so. Always rebuilds."""
     hipcc = find_hipcc()
+    digest = source_digest()   # of the sources as compiled: an edit made during the build leaves it stale
     BUILD_DIR.mkdir(parents=True, exist_ok=True)
     LIB_DIR.mkdir(parents=True, exist_ok=True)
     srcs = sources()
@@ -109,7 +110,7 @@ def build(verbose: bool = False, jobs: int | None = None) -> Path:
     if proc.returncode != 0:
         raise BuildError("link failed:\n" + proc.stdout + proc.stderr)
     os.replace(tmp, out)
-    (LIB_DIR / "BUILD_DIGEST").write_text(source_digest() + "\n", encoding="utf-8")
+    (LIB_DIR / "BUILD_DIGEST").write_text(digest + "\n", encoding="utf-8")
     return out
 
 

@@ -33,6 +33,8 @@ MB_ERR_WORKSPACE = -4
 MB_ERR_DEVICE = -5
 
 NOALLOC_SCRATCH_BYTES = 64 << 20   # MB_NOALLOC_SCRATCH_BYTES
+CLOCK_BLOCKS = 1024                # MB_CLOCK_BLOCKS
+CLOCK_REALTIME_HZ = 100_000_000    # MB_CLOCK_REALTIME_HZ
 
 OP_COPY, OP_SCALE, OP_TRIAD = 0, 1, 2
 OPS = {"copy": OP_COPY, "scale": OP_SCALE, "triad": OP_TRIAD}
@@ -118,6 +120,7 @@ SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
         [ctypes.c_int, ctypes.c_int, ctypes.c_int, _i64, _i64, _i64, ctypes.c_char_p, ctypes.c_size_t],
     ),
     "mb_set_tuning": (ctypes.c_int, [ctypes.c_int, _i64]),
+    "mb_clock_stamp": (ctypes.c_int, [_vp, _vp]),
     "mb_get_tuning": (_i64, [ctypes.c_int]),
 }
 
@@ -218,6 +221,11 @@ class NativeLibrary:
 
     def gemm_info(self, dtype: int, m: int, n: int, k: int) -> dict[str, Any]:
         return self.kernel_info(KIND_GEMM, dtype, 0, m, n, k)
+
+    # ---- clock stamps ------------------------------------------------------
+    def clock_stamp(self, out: int, stream: int | None = None) -> None:
+        """Enqueue one stamp (4 * CLOCK_BLOCKS uint64 at device address `out`): see mb_clock_stamp."""
+        self._check(self.handle.mb_clock_stamp(out, stream or None), "mb_clock_stamp")
 
     # ---- plan overrides ----------------------------------------------------
     def set_tuning(self, knob: str, value: int | None) -> None:

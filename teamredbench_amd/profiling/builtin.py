@@ -23,11 +23,17 @@ per-kernel summary attached to the metadata sidecar:
 
 Params (suite ``profiling.params``): binary (default rocprofv3), stats
 (bool, default true), kernel_include_regex, counter_passes (list of counter
-lists; default the three passes above; [] disables counters), hip_trace
-(bool; only on the trace pass), calibrate (bool, default true), extra_args,
-env.
+lists; default the three passes above; [] disables counters), hip_trace,
+hsa_trace, marker_trace, sys_trace (bools; only on the trace pass, never
+beside counters), truncate_kernels (bool), calibrate (bool, default true),
+extra_args, env.
+
 The engine is registered as ``rocprofv3`` and, for suites written for the
-reference, as ``rocprof``.
+reference, as ``rocprof``. The ``rocprof`` name takes the reference engine's
+v1 parameters (src/teamredbench/profiling/builtin.py:37-143) and translates
+each one that rocprofv3 can honour (:func:`translate_v1_params`); a suite
+that sets one it cannot honour fails with an error naming every such
+parameter, instead of running without what it asked for.
 """
 from __future__ import annotations
 
@@ -43,6 +49,10 @@ from typing import Any
 from teamredbench_amd.profiling.registry import ProfilingLaunch, register_profile_engine
 
 DEFAULT_COUNTER_PASSES = [["FETCH_SIZE"], ["WRITE_SIZE"], ["SQ_VALU_MFMA_BUSY_CYCLES", "GRBM_GUI_ACTIVE"]]
+# API-trace domains: added to the kernel-trace pass only. No counter pass ever carries them (a counter
+# collection combined with an API trace in one profiler run is not supported on this platform).
+TRACE_ONLY_FLAGS = {"hip_trace": "--hip-trace", "hsa_trace": "--hsa-trace", "marker_trace": "--marker-trace",
+                    "sys_trace": "--sys-trace"}
 SIMDS_PER_CU = 4
 CALIBRATION_ELEMENTS = 1 << 26          # fp32 copy: reads and writes 256 MiB
 CALIBRATION_KERNEL = "stream_vec_kernel<0, "  # the library's copy kernel
@@ -79,8 +89,11 @@ def _build_rocprofv3_command(params: dict[str, Any], target_command: list[str], 
     trace = [binary, "--kernel-trace", "-d", str(artifact_dir / "trace"), "-o", "run"]
     if params.get("stats", True):
         trace.append("--stats")
-    if params.get("hip_trace"):
-        trace.append("--hip-trace")
+    for key, flag in TRACE_ONLY_FLAGS.items():
+        if params.get(key):
+            trace.append(flag)
+    if params.get("truncate_kernels"):
+        trace.append("--truncate-kernels")
     trace += _common(params) + ["--"]
 
     passes = params.get("counter_passes", DEFAULT_COUNTER_PASSES)
@@ -249,8 +262,106 @@ register_profile_engine(
     description="Profile a run with rocprofv3: kernel trace plus FETCH/WRITE_SIZE and MFMA-busy counter passes.",
     build_command=_build_rocprofv3_command,
 )
+# ---------------------------------------------------------------- the reference's v1 parameters
+# What the `rocprof` name does with each parameter of the reference's engine
+# (src/teamredbench/profiling/builtin.py:37-143) that has no rocprofv3 counterpart here: the reason it is
+# refused.
+V1_REFUSED = {
+    "tool_version": "selects between rocprof v1 and v2; this engine always drives rocprofv3",
+    "metric_file": "names a v1 derived-metric XML file, which rocprofv3 does not read",
+    "output": "names the v1 CSV file; rocprofv3 writes its CSVs under the run's artifact directory "
+              "(outputs.profiling in the sidecar)",
+    "data_dir": "names the v1 data directory; the artifact directory holds rocprofv3's data",
+    "temporary_dir": "names the v1 temporary directory, which rocprofv3 does not use",
+    "cmd_qts": "is a v1 toggle with no rocprofv3 option",
+    "ctx_wait": "is a v1 toggle with no rocprofv3 option",
+    "obj_tracking": "is a v1 toggle with no rocprofv3 option",
+    "trace_start": "is a v1 toggle with no rocprofv3 option",
+    "ctx_limit": "is a v1 option with no rocprofv3 counterpart",
+    "heartbeat": "is a v1 option with no rocprofv3 counterpart",
+    "trace_period": "is a v1 option with no rocprofv3 counterpart",
+    "flush_rate": "is a v1 option with no rocprofv3 counterpart",
+    "roctx_rename": "is a v1 flag with no rocprofv3 counterpart",
+    "parallel_kernels": "is a v1 flag with no rocprofv3 counterpart",
+}
+V1_BINARIES = ("rocprof", "rocprofv2")
+
+
+def read_v1_input(path: Path) -> tuple[list[list[str]], list[str], list[str]]:
+    """A rocprof v1 counter input file: each ``pmc:`` line is one pass of counters (separated by spaces or
+    commas), each ``kernel:`` line adds kernel names to profile; returns (passes, kernels, refused
+    directives). ``#`` starts a comment."""
+    passes: list[list[str]] = []
+    kernels: list[str] = []
+    refused: list[str] = []
+    for raw in path.read_text(encoding="utf-8").splitlines():
+        line = raw.split("#", 1)[0].strip()
+        if not line:
+            continue
+        key, sep, rest = line.partition(":")
+        names = [x for x in rest.replace(",", " ").split() if x]
+        key = key.strip().lower()
+        if sep and key == "pmc" and names:
+            passes.append(names)
+        elif sep and key == "kernel" and names:
+            kernels += names
+        else:
+            refused.append(line)
+    return passes, kernels, refused
+
+
+def translate_v1_params(params: dict[str, Any], base_dir: Path | None) -> dict[str, Any]:
+    """The rocprofv3 engine's params for a suite written for the reference's rocprof (v1) engine.
+
+    Translated: stats, hip_trace, hsa_trace, sys_trace (same meaning, on the kernel-trace pass),
+    roctx_trace (-> marker_trace), basenames on (-> truncate_kernels), timestamp on (rocprofv3 always
+    records timestamps), input (a v1 counter file: its ``pmc:`` lines become the counter passes and its
+    ``kernel:`` lines the kernel filter), binary (unless it names the v1/v2 tool), env, extra_args (handed
+    to rocprofv3 as they are). Every other v1 parameter, and timestamp / basenames off, raises ValueError
+    naming each one and why."""
+    out: dict[str, Any] = {}
+    errors: list[str] = []
+    for key, value in params.items():
+        if key in V1_REFUSED:
+            errors.append(f"{key} {V1_REFUSED[key]}")
+        elif key == "roctx_trace":
+            out["marker_trace"] = bool(value)
+        elif key == "basenames":
+            if bool(value):
+                out["truncate_kernels"] = True
+        elif key == "timestamp":
+            if not bool(value):
+                errors.append("timestamp: off cannot be honoured; rocprofv3 always records kernel timestamps")
+        elif key == "binary" and Path(str(value)).name in V1_BINARIES:
+            errors.append(f"binary {value!r} is the v1/v2 profiler, whose flags differ; name rocprofv3 or leave "
+                          "binary out")
+        elif key == "input":
+            path = _resolve(base_dir, str(value))
+            try:
+                passes, kernels, refused = read_v1_input(path)
+            except OSError as exc:
+                errors.append(f"input {str(path)!r} cannot be read: {exc}")
+                continue
+            for line in refused:
+                errors.append(f"input {path.name}: {line!r} is not a pmc: or kernel: line")
+            if passes:
+                out["counter_passes"] = passes
+            if kernels:
+                out["kernel_include_regex"] = "|".join(kernels)
+        else:
+            out[key] = value
+    if errors:
+        raise ValueError("profiling.params for the rocprof engine: " + "; ".join(errors))
+    return out
+
+
+def _build_rocprof_v1_command(params: dict[str, Any], target_command: list[str], artifact_dir: Path,
+                              base_dir: Path | None) -> ProfilingLaunch:
+    return _build_rocprofv3_command(translate_v1_params(params, base_dir), target_command, artifact_dir, base_dir)
+
+
 register_profile_engine(
     name="rocprof",
-    description="Alias of rocprofv3 for suites written for the reference's rocprof engine.",
-    build_command=_build_rocprofv3_command,
+    description="rocprofv3, taking the reference rocprof engine's v1 parameters (translated, or refused by name).",
+    build_command=_build_rocprof_v1_command,
 )

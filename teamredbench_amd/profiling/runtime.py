@@ -41,6 +41,10 @@ from teamredbench_amd.profiling.registry import ProfilingLaunch, get_profile_eng
 INTERNAL_RUN_ENV = "TEAMREDBENCH_INTERNAL_RUN"
 FORCE_JSON_OUTPUT_ENV = "TEAMREDBENCH_FORCE_JSON_OUTPUT"
 RUN_TOKEN_ENV = "TEAMREDBENCH_RUN_TOKEN"
+# The hardware profile the parent resolved for a suite whose own profile has no peaks, and the note saying
+# so: the child under the profiler measures against the same profile instead of detecting it again.
+RESOLVED_PROFILE_ENV = "TEAMREDBENCH_RESOLVED_HARDWARE_PROFILE"
+RESOLVED_NOTE_ENV = "TEAMREDBENCH_RESOLVED_PROFILE_NOTE"
 
 
 class ProfilingError(RuntimeError):
@@ -62,6 +66,12 @@ def effective_output_formats(formats: list[str]) -> list[str]:
     return list(formats) + (["json"] if forced and "json" not in formats else [])
 
 
+def inherited_hardware_profile() -> tuple[Path, str] | None:
+    """Inside the child of a profiled run: the (profile path, note) its parent resolved, if it did."""
+    path = os.environ.get(RESOLVED_PROFILE_ENV) if profiling_active() else None
+    return (Path(path), os.environ.get(RESOLVED_NOTE_ENV, "")) if path else None
+
+
 def run_token() -> str | None:
     """The token a profiled run's parent gave this process (recorded in the sidecar)."""
     return os.environ.get(RUN_TOKEN_ENV)
@@ -73,7 +83,8 @@ def child_command(suite_path: Path, device_id: int, output_dir: Path) -> list[st
 
 
 class ProfiledRun:
-    def __init__(self, suite: SuiteConfig, output_dir: Path, device_id: int):
+    def __init__(self, suite: SuiteConfig, output_dir: Path, device_id: int, resolved_profile: Path | None = None,
+                 profile_note: str | None = None):
         if suite.path is None:
             raise ProfilingError("Suite path is required for profiled runs.")
         if not suite.profiling.engine:
@@ -84,6 +95,8 @@ class ProfiledRun:
         self.artifact_dir = self.output_dir / "profiling" / f"{suite.name}-{self.engine.name}-{stamp}"
         self.token = uuid.uuid4().hex
         self.env = {**os.environ, INTERNAL_RUN_ENV: "1", FORCE_JSON_OUTPUT_ENV: "1", RUN_TOKEN_ENV: self.token}
+        if resolved_profile is not None and profile_note:
+            self.env.update({RESOLVED_PROFILE_ENV: str(resolved_profile), RESOLVED_NOTE_ENV: profile_note})
         self.launch_spec: ProfilingLaunch | None = None
         self.teardown_crashes: list[dict[str, Any]] = []
 
@@ -159,10 +172,12 @@ class ProfiledRun:
 
 
 def run_profiled_suite(*, suite: SuiteConfig, context: BenchmarkContext, output_dir: Path, device_id: int,
-                       record_callback):
+                       record_callback, profile_note: str | None = None):
     from teamredbench_amd.runner import RunSummary
 
-    run = ProfiledRun(suite, output_dir, device_id)
+    # A profile the parent auto-selected goes to the child with its note.
+    resolved = getattr(context.hardware_profile, "path", None) if profile_note else None
+    run = ProfiledRun(suite, output_dir, device_id, resolved_profile=resolved, profile_note=profile_note)
     run.launch()
     sidecar_path = run.sidecar_path()
     try:
@@ -179,4 +194,5 @@ def run_profiled_suite(*, suite: SuiteConfig, context: BenchmarkContext, output_
     run_metadata = dict(sidecar["run"])
     return RunSummary(suite=suite, context=context, records=records,
                       outputs={name: Path(p) for name, p in sidecar["outputs"].items()},
-                      run_metadata=run_metadata, profile_note=run_metadata.get("configs", {}).get("profile_note"))
+                      run_metadata=run_metadata,
+                      profile_note=run_metadata.get("configs", {}).get("profile_note") or profile_note)

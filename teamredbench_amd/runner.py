@@ -7,7 +7,9 @@ steps. Two behaviours carried over:
   * the device index is ``LOCAL_RANK`` when that is set, else ``device_id``;
   * a hardware profile with no peak data (hbm bandwidth and at least one
     compute peak) is replaced by a profile whose SKU token (``mi355x`` ...)
-    matches the detected device name, found by :class:`ProfileCatalog` in
+    matches the detected device name (torch's, or, when that carries no
+    SKU, the product names amdsmi and rocm-smi report for the device:
+    device.product_names), found by :class:`ProfileCatalog` in
     the suite tree's ``configs/profiles/hardware`` or among this package's
     profiles; the replacement is reported in ``profile_note``.
 Metrics are derived only for ``ok`` records; a skipped or failed record keeps
@@ -25,10 +27,15 @@ from typing import Callable, Iterable
 from teamredbench_amd import builtin as _builtin  # noqa: F401  (registers the built-in benchmarks and metrics)
 from teamredbench_amd.benchmarks.base import BenchmarkContext, BenchmarkRecord
 from teamredbench_amd.config import HardwareProfile, SuiteConfig, load_hardware_profile, load_suite
-from teamredbench_amd.device import detect_device, load_torch
+from teamredbench_amd.device import detect_device, load_torch, product_names
 from teamredbench_amd.dtypes import discover_dtypes
 from teamredbench_amd.io import write_results
-from teamredbench_amd.profiling.runtime import effective_output_formats, profiling_enabled, run_profiled_suite
+from teamredbench_amd.profiling.runtime import (
+    effective_output_formats,
+    inherited_hardware_profile,
+    profiling_enabled,
+    run_profiled_suite,
+)
 from teamredbench_amd.provenance import build_run_metadata
 from teamredbench_amd.registry import get_benchmark, get_metric, load_plugins
 
@@ -99,10 +106,19 @@ def build_context(suite: SuiteConfig, device_id: int = 0) -> tuple[BenchmarkCont
     torch_module = load_torch()
     device = detect_device(torch_module, device_id=index)
     profile, note = suite.hardware_profile, None
-    if not has_peak_data(profile) and device is not None:
-        stand_in = ProfileCatalog.for_suite(_suite_repo_root(suite)).match(device.name)
+    inherited = inherited_hardware_profile() if not has_peak_data(profile) else None
+    if inherited is not None:
+        # the child of a profiled run measures against the profile its parent resolved
+        profile, note = load_hardware_profile(inherited[0]), inherited[1]
+    elif not has_peak_data(profile) and device is not None:
+        # torch's device name carries the SKU where the platform's marketing-name table is installed;
+        # otherwise the board's own product name (amdsmi, rocm-smi) does
+        detected = device.name
+        if not sku_tokens(detected):
+            detected = " / ".join([device.name, *product_names(torch_module, index)])
+        stand_in = ProfileCatalog.for_suite(_suite_repo_root(suite)).match(detected)
         if stand_in is not None:
-            note = (f"Auto-selected hardware profile {stand_in.name} from detected device {device.name!r} "
+            note = (f"Auto-selected hardware profile {stand_in.name} from detected device {detected!r} "
                     f"because {profile.name} has no theoretical peak data.")
             profile = stand_in
     context = BenchmarkContext(
@@ -170,6 +186,7 @@ def run_suite(suite_path: str | Path, output_dir: str | Path | None = None, devi
     if profiling_enabled(run.suite.profiling):
         # the whole suite runs again in a child process under the profiler
         return run_profiled_suite(suite=run.suite, context=run.context, output_dir=run.output_dir,
-                                  device_id=device_id, record_callback=record_callback)
+                                  device_id=device_id, record_callback=record_callback,
+                                  profile_note=run.profile_note)
     run.execute()
     return run.finish()

@@ -68,6 +68,8 @@ def test_abi_constants_match_the_header():
     assert int(consts["MB_TUNE_COUNT"]) == len(capi.TUNING_KNOBS)
     shift = re.search(r"#define MB_NOALLOC_SCRATCH_BYTES \((\d+)u << (\d+)\)", text)
     assert shift and int(shift.group(1)) << int(shift.group(2)) == capi.NOALLOC_SCRATCH_BYTES
+    assert int(consts["MB_CLOCK_BLOCKS"]) == capi.CLOCK_BLOCKS
+    assert int(consts["MB_CLOCK_REALTIME_HZ"]) == capi.CLOCK_REALTIME_HZ
 
 
 def test_tuning_knobs_validate_and_restore_without_a_gpu():

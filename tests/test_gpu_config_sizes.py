@@ -12,7 +12,11 @@ plans) have oracle-checked output:
     shapes 8192 x 1024 x 8192 and 4096 x 14336 x 4096 in bf16 and fp16: a
     seeded subset of C's rows (every column) against the fp32 CPU matmul of
     the same (dequantised) operands, with the relative-Frobenius gates of the
-    configurations (1e-2 bf16/fp16, 5e-2 fp8), plus a per-element bound;
+    configurations (1e-2 bf16/fp16, 5e-2 fp8), and every element of those
+    rows within its rounding bound of an fp64 matmul of the same operands
+    (tests/gemm_bounds.py: output half-ulp, (K + 2) fp32 summation steps of
+    |A| @ |B|, the fp8 MFMA block term), which a tile that skipped one of its
+    K stages, or took one from the wrong place, fails;
   * the reference's own numerical parity case
     (tests/native/gemm_parity.hip.cpp:126-130, 174-178;
     tests/test_native_gemm_parity.py:69): A from std::mt19937(0xA1), B from
@@ -30,6 +34,7 @@ import numpy as np
 import pytest
 import torch
 
+from gemm_bounds import elementwise_bound
 from oracle import clib
 from oracle import reference_path as rp
 from teamredbench_amd.native import capi
@@ -112,12 +117,20 @@ def test_gemm_configuration_shape_matches_oracle(lib, dtype, shape):
     out = got[rows].float()
     err = rp.rel_frobenius(out, ref)
     assert err <= REL_FROB[dtype], f"{dtype} {shape}: rel-Frobenius {err:.3e} over {rows.numel()} rows"
-    # every checked element also within a per-element bound, which catches a few corrupted tiles that the
-    # Frobenius norm would average away: the reference multiplies the same (dequantised) operands, so an
-    # element differs by its output rounding (2^-9 relative for bf16) and fp32 summation order only, far
-    # below 5% of max|C|; an element taken from a wrong tile is off by about max|C| / 5
-    scale = float(ref.abs().max())
-    assert float((out - ref).abs().max()) <= 0.05 * scale, f"{dtype} {shape}: an element is far off"
+    # Every checked element within its rounding bound of the fp64 product of the same operands (exact
+    # inputs, so only fp64 rounding separates it from the true sum). The magnitude term |A_rows| @ |B| is
+    # taken in fp32 (every term is positive, so its own rounding is below (K + 2) * 2^-24 relative: the
+    # bound's slack factor 1 + 2^-8 covers it at K <= 16384).
+    s = float(ops["scale_a"]) * float(ops["scale_b"])
+    ref64 = s * (ops["a"][rows].double() @ ops["b"].double())
+    mag = s * (ops["a"][rows].float().abs() @ ops["b"].float().abs()).double() * (1.0 + 2.0**-8)
+    bound = elementwise_bound(dtype, k, ref64.abs(), mag)
+    excess = (got[rows].double() - ref64).abs() - bound
+    worst = int(torch.argmax(excess))
+    wr, wc = divmod(worst, n)
+    assert float(excess.max()) <= 0.0, (
+        f"{dtype} {shape}: C[{int(rows[wr])}, {wc}] = {float(got[rows][wr, wc])!r}, fp64 {float(ref64[wr, wc])!r}, "
+        f"bound {float(bound[wr, wc]):.3e}")
 
 
 @pytest.mark.parametrize("dtype", ["float16", "bfloat16", "float32", "float64"])

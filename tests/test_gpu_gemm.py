@@ -651,3 +651,13 @@ def test_kernel_info_names_the_fallback(lib, dtype, shape, impl, reason):
     info = lib.gemm_info(capi.DTYPES[dtype], *shape)
     assert info["implementation"].startswith(impl) and info["fallback"] == reason
     _check_random(lib, dtype, *shape, seed=1)
+
+
+@pytest.mark.parametrize("dtype, shape", [("float32", (1 << 31, 4, 4)), ("float64", (1 << 31, 2, 2)),
+                                          ("float32", ((1 << 31) + 256, 256, 16))])
+def test_highp_rows_past_int32_take_the_register_staged_kernel(lib, dtype, shape):
+    # Plan only, nothing launched: the LDS-DMA kernels index rows with int, so M >= 2^31 must fall back
+    # to the register-staged kernel (int64 indexes) and say why.
+    info = lib.gemm_info(capi.DTYPES[dtype], *shape)
+    assert not info["implementation"].endswith("lds_dma"), info
+    assert "2^31" in info["fallback"], info

@@ -61,10 +61,10 @@ def test_suite_runs_end_to_end(tmp_path: Path, backend: str):
         if backend == "native":
             assert record.metadata["parity"]["passed"] is True, (record.case, record.metadata["parity"])
     skinny = [r for r in records if r.case == "gemm_16x8192x1024"]
-    if backend == "native":
-        # memory-bound and cache-sized: timed over operand copies that exceed the Infinity Cache
-        assert all(r.metadata["operand_sets"] > 1 and r.metadata["cache_resident_b"] is False for r in skinny)
-    else:
+    # memory-bound and cache-sized: both backends time it over operand copies that exceed the Infinity Cache
+    assert all(r.metadata["operand_sets"] > 1 and r.metadata["cache_resident_b"] is False
+               and r.metadata["operand_footprint_bytes"] >= 3 * 256 * (1 << 20) for r in skinny)
+    if backend == "torch":
         fp8 = next(r for r in skinny if r.dtype == "float8_e4m3fn")
         assert fp8.metadata["torch_op"] == "_scaled_mm"
     for fmt in ("json", "csv", "metadata"):
@@ -92,6 +92,10 @@ def test_profiled_suite_attaches_counters(tmp_path: Path):
     summary = run_suite(_write_suite(tmp_path, "profiled", benchmarks, profiling))
     assert [r.status for r in summary.records] == ["ok", "ok"], [r.error for r in summary.records]
     sidecar = json.loads(summary.outputs["metadata"].read_text(encoding="utf-8"))
+    # A profiler exit by SIGSEGV after complete output is tolerated and recorded, never silent.
+    crashes = sidecar["run"]["profiling"].get("profiler_teardown_crashes", [])
+    print(f"[suite] profiler_teardown_crashes: {crashes}", flush=True)
+    assert all(c["exit_status"] in (-11, 139) and c["step"] for c in crashes), crashes
     counters = sidecar["run"]["profiling"]["counters"]
     assert set(counters["_calibration"]) == {"FETCH_SIZE", "WRITE_SIZE"}
     triad = [v for k, v in counters.items() if "stream_vec_kernel<2, 0" in k]

@@ -368,7 +368,17 @@ def test_record_round_trips_through_its_result_forms():
     assert BenchmarkRecord.from_dict(json.loads(json.dumps(record.to_dict()))) == record
     row = record.to_row()
     assert row["metric_mfu_pct"] == 1.5 and row["error"] == ""
-    assert json.loads(row["meta_parity"]) == {"passed": True} and json.loads(row["meta_shape"]) == [8, 8, 8]
+    # nested values reach the CSV as the reference writes them: str(value), Python's text of the value
+    import ast
+    import csv
+    import io as _io
+
+    buf = _io.StringIO()
+    writer = csv.DictWriter(buf, fieldnames=list(row))
+    writer.writeheader()
+    writer.writerow(row)
+    cells = next(csv.DictReader(_io.StringIO(buf.getvalue())))
+    assert cells["meta_parity"] == "{'passed': True}" and ast.literal_eval(cells["meta_shape"]) == [8, 8, 8]
 
 
 def test_unknown_output_formats_are_reported_not_fatal(tmp_path: Path):
@@ -420,3 +430,108 @@ def test_example_executable_is_prebuilt_under_the_key_a_suite_resolves():
     cache = native_runtime.KernelCache(kernel.cache_dir)
     expected = cache.directory / f"{kernel.name}-{cache.key(kernel, native_runtime._find_hip_compiler())}"
     assert expected in build.build_examples() and expected.exists()
+
+
+# ---------------------------------------------------------------- mfu operand sets
+def _mfu(params: dict):
+    from teamredbench_amd.benchmarks.mfu import MfuBenchmark
+
+    profile = load_hardware_profile(HW_DIR / "amd_instinct_mi355x.yaml")
+    return MfuBenchmark(context=SimpleNamespace(hardware_profile=profile), params=params)
+
+
+def _spec(name: str, size: int):
+    return SimpleNamespace(name=name, bytes_per_element=size, matmul_ops_factor=2)
+
+
+def test_operand_sets_span_three_infinity_caches_counting_a_b_and_c():
+    from teamredbench_amd.benchmarks.mfu import INFINITY_CACHE_BYTES, OPERAND_FOOTPRINT_TARGET, gemm_bytes
+
+    bench = _mfu({})
+    # 64 x 1024 x 1024 bf16: 2.25 MiB per set (A + B + C), far under the cache; memory-bound
+    sets, info = bench._operand_sets(_spec("bfloat16", 2), 64, 1024, 1024, 2, 2500.0)
+    per_set = gemm_bytes(64, 1024, 1024, 2, 2)
+    assert sets == -(-OPERAND_FOOTPRINT_TARGET // per_set) and sets > 64
+    assert info["operand_footprint_bytes"] == sets * per_set >= OPERAND_FOOTPRINT_TARGET
+    assert info["cache_resident_b"] is False and "operand_footprint_short_of_target" not in info
+    # small K, large M x N: C dominates the set, so fewer copies reach the target (no 64 copies of C)
+    sets, info = bench._operand_sets(_spec("bfloat16", 2), 8192, 8192, 16, 2, 2500.0)
+    assert sets == -(-OPERAND_FOOTPRINT_TARGET // gemm_bytes(8192, 8192, 16, 2, 2)) <= 7
+    # compute-bound: one set; the footprint decides residency (8192^3 bf16 spans 384 MiB)
+    sets, info = bench._operand_sets(_spec("bfloat16", 2), 4096, 4096, 4096, 2, 2500.0)
+    assert (sets, info["cache_resident_b"]) == (1, True)
+    sets, info = bench._operand_sets(_spec("bfloat16", 2), 8192, 8192, 8192, 2, 2500.0)
+    assert (sets, info["cache_resident_b"]) == (1, False)
+    # a set beyond the target is already streamed from HBM
+    assert bench._operand_sets(_spec("bfloat16", 2), 1, 32768, 16384, 2, 2500.0)[0] == 1
+    assert INFINITY_CACHE_BYTES == 256 << 20
+
+
+def test_operand_sets_cap_is_reported_and_a_count_is_taken_as_given():
+    from teamredbench_amd.benchmarks.mfu import MAX_OPERAND_SETS
+
+    sets, info = _mfu({})._operand_sets(_spec("bfloat16", 2), 16, 256, 256, 2, 2500.0)   # 144 KiB per set
+    assert sets == MAX_OPERAND_SETS and info["operand_footprint_short_of_target"] is True
+    sets, info = _mfu({"operand_sets": 1})._operand_sets(_spec("bfloat16", 2), 64, 1024, 1024, 2, 2500.0)
+    assert sets == 1 and info["cache_resident_b"] is True
+    assert _mfu({"operand_sets": 5})._operand_sets(_spec("float8_e4m3fn", 1), 8, 8, 8, 2, 5000.0)[0] == 5
+
+
+def test_generic_profile_found_from_the_board_name_when_torch_has_none(monkeypatch):
+    # Where libdrm's marketing-name table is missing, torch names the device without its SKU; the board's
+    # product name (amdsmi / rocm-smi) then identifies it.
+    monkeypatch.setattr(runner_mod, "load_torch", lambda: object())
+    monkeypatch.setattr(runner_mod, "detect_device",
+                        lambda torch_module, device_id=0: DeviceInfo(index=0, name="AMD Radeon Graphics"))
+    monkeypatch.setattr(runner_mod, "product_names", lambda torch_module, index: ["AMD Instinct MI355X OAM"])
+    context, note = runner_mod.build_context(load_suite(PACKAGE / "configs" / "suites" / "native_smoke.yaml"))
+    assert context.hardware_profile.name == "amd-instinct-mi355x"
+    assert "MI355X OAM" in note
+    monkeypatch.setattr(runner_mod, "product_names", lambda torch_module, index: [])
+    context, note = runner_mod.build_context(load_suite(PACKAGE / "configs" / "suites" / "native_smoke.yaml"))
+    assert context.hardware_profile.name == "cdna-generic" and note is None
+
+
+def test_amdsmi_names_include_the_gfx950_sku_of_the_peak_clock(monkeypatch):
+    import sys as _sys
+
+    from teamredbench_amd import device as device_mod
+
+    class FakeSmi:
+        class AmdSmiClkType:
+            GFX = "gfx"
+
+        max_clk = 2400
+
+        def amdsmi_init(self):
+            pass
+
+        def amdsmi_shut_down(self):
+            pass
+
+        def amdsmi_get_processor_handles(self):
+            return ["h0", "h1"]
+
+        def amdsmi_get_gpu_device_bdf(self, h):
+            return {"h0": "0000:11:00.0", "h1": "0000:f1:00.0"}[h]
+
+        def amdsmi_get_gpu_board_info(self, h):
+            return {"product_name": "N/A"}
+
+        def amdsmi_get_gpu_asic_info(self, h):
+            return {"market_name": "AMD Radeon Graphics"}
+
+        def amdsmi_get_clock_info(self, h, kind):
+            assert h == "h1"
+            return {"max_clk": self.max_clk}
+
+    fake = FakeSmi()
+    props = SimpleNamespace(pci_domain_id=0, pci_bus_id=0xF1, pci_device_id=0, gcnArchName="gfx950:sramecc+:xnack-")
+    torch_like = SimpleNamespace(cuda=SimpleNamespace(get_device_properties=lambda i: props))
+    monkeypatch.setitem(_sys.modules, "amdsmi", fake)
+    names = device_mod._amdsmi_names(torch_like, 0)
+    assert names[0] == "AMD Radeon Graphics" and "MI355X" in names[1]
+    fake.max_clk = 2200
+    assert "MI350X" in device_mod._amdsmi_names(torch_like, 0)[-1]
+    fake.max_clk = 2100
+    assert device_mod._amdsmi_names(torch_like, 0) == ["AMD Radeon Graphics"]

@@ -230,3 +230,114 @@ def test_waits_summary_shares_of_wave_cycles(tmp_path: Path):
     assert "%" not in by_name["GRBM_GUI_ACTIVE"]
     with pytest.raises(SystemExit):
         summarize.waits(tmp_path / "sq", "no_such_kernel")
+
+
+# ---- the reference engine's v1 parameters under the `rocprof` name (src/teamredbench/profiling/builtin.py:37-143)
+def test_rocprof_name_translates_the_reference_smoke_params(tmp_path: Path):
+    # configs/suites/rocprof_hbm_smoke.yaml: engine rocprof, params {stats: true, hip_trace: true}
+    launch = get_profile_engine("rocprof").build_command({"stats": True, "hip_trace": True}, ["x"], tmp_path, None)
+    assert launch.command[1] == "--kernel-trace"
+    assert "--stats" in launch.command and "--hip-trace" in launch.command
+    assert launch.metadata["binary"].endswith("rocprofv3")
+    for prefix in launch.extra_passes:     # the API trace stays off the counter passes
+        assert "--hip-trace" not in prefix and "--stats" not in prefix
+
+
+def test_rocprof_name_translates_trace_toggles(tmp_path: Path):
+    params = {"roctx_trace": True, "hsa_trace": True, "sys_trace": True, "basenames": True, "timestamp": True,
+              "env": {"A": "1"}, "extra_args": ["--minimum-output-data", "0"]}
+    launch = get_profile_engine("rocprof").build_command(params, ["x"], tmp_path, None)
+    trace = launch.command[:launch.command.index("--")]
+    for flag in ("--marker-trace", "--hsa-trace", "--sys-trace", "--truncate-kernels", "--minimum-output-data"):
+        assert flag in trace
+    assert launch.env["A"] == "1"
+    for prefix in launch.extra_passes:
+        assert not any(a.endswith("-trace") for a in prefix)
+
+
+def test_rocprof_name_reads_a_v1_counter_input_file(tmp_path: Path):
+    suite_dir = tmp_path / "suites"
+    suite_dir.mkdir()
+    (suite_dir / "counters.txt").write_text(
+        "# v1 input\npmc: FETCH_SIZE\npmc : WRITE_SIZE, GRBM_GUI_ACTIVE\nkernel: stream_vec_kernel gemm_tiled\n",
+        encoding="utf-8")
+    launch = get_profile_engine("rocprof").build_command({"input": "counters.txt"}, ["x"], tmp_path / "a", suite_dir)
+    passes = [list(p[p.index("--pmc") + 1:p.index("-d")]) for p in launch.extra_passes]
+    assert passes == [["FETCH_SIZE"], ["WRITE_SIZE", "GRBM_GUI_ACTIVE"]]
+    assert launch.command[launch.command.index("--kernel-include-regex") + 1] == "stream_vec_kernel|gemm_tiled"
+    (suite_dir / "bad.txt").write_text("pmc: FETCH_SIZE\nrange: 0:10\ngpu: 0\n", encoding="utf-8")
+    with pytest.raises(ValueError) as err:
+        get_profile_engine("rocprof").build_command({"input": "bad.txt"}, ["x"], tmp_path / "b", suite_dir)
+    assert "'range: 0:10'" in str(err.value) and "'gpu: 0'" in str(err.value)
+
+
+def test_rocprof_name_refuses_what_rocprofv3_cannot_honour(tmp_path: Path):
+    params = {name: ("x" if name in ("tool_version", "metric_file", "output", "data_dir", "temporary_dir") else True)
+              for name in builtin.V1_REFUSED}
+    params.update({"timestamp": False, "binary": "rocprof"})
+    with pytest.raises(ValueError) as err:
+        get_profile_engine("rocprof").build_command(params, ["x"], tmp_path, None)
+    message = str(err.value)
+    for name in [*builtin.V1_REFUSED, "timestamp", "binary"]:
+        assert name in message, name
+    # the rocprofv3 engine itself takes its own parameters only
+    assert get_profile_engine("rocprofv3").build_command({"stats": False}, ["x"], tmp_path / "v3", None)
+
+
+def test_clock_summary_pairs_stamps_cu_by_cu():
+    from teamredbench_amd.profiling.clock import clock_summary
+
+    # two XCDs x 4 CUs, counters offset per CU by ~1e8 cycles; XCD 0 at 1500 MHz, XCD 1 at 2000 MHz over
+    # 10 ms (1e6 ticks of the 100 MHz counter); the second stamp lands its blocks in another order
+    def stamp(t_real: int, order: list[int]) -> list[list[int]]:
+        rows = []
+        for i in order:
+            xcd, cu = divmod(i, 4)
+            offset = 10**8 * (i + 1)
+            shader = offset + (1500 if xcd == 0 else 2000) * t_real // 100
+            rows.append([shader, 5_000_000 + t_real, xcd, (cu << 8) | 0x25])
+        return rows
+
+    before = stamp(0, list(range(8)) + [0, 5])         # CU 0 and CU 5 ran two blocks
+    after = stamp(1_000_000, [7, 6, 5, 4, 3, 2, 1])   # CU 0 missing from the second stamp
+    out = clock_summary(before, after)
+    assert out["gfxclk_mhz_per_xcd"] == {"0": 1500.0, "1": 2000.0}
+    assert out["cus_paired"] == 7 and out["cu_spread_mhz"] == 0.0 and out["window_s"] == 0.01
+    assert clock_summary(before, [])["available"] is False
+
+
+def test_profiled_child_measures_against_the_profile_its_parent_resolved(tmp_path: Path, monkeypatch):
+    # The parent auto-selects the MI355X profile for a suite whose own profile has no peaks; the child under
+    # the profiler (a separate process, which here sees no device at all) measures against the same one.
+    from teamredbench_amd import runner as runner_mod
+    from teamredbench_amd.device import DeviceInfo
+
+    profiler = tmp_path / "fake_rocprofv3.py"
+    profiler.write_text(FAKE_PROFILER.replace("COPY if", f"{COPY!r} if").replace("else TRIAD", f"else {TRIAD!r}"),
+                        encoding="utf-8")
+    profiler.chmod(0o755)
+    executable = tmp_path / "fake_hbm.py"
+    executable.write_text("#!/usr/bin/env python3\nimport json\n"
+                          "print(json.dumps({'status': 'ok', 'raw_metrics': {'elapsed_s': 0.001}}))\n",
+                          encoding="utf-8")
+    executable.chmod(0o755)
+    generic = runner_mod.PACKAGED_HARDWARE_DIR / "cdna_generic.yaml"
+    runtime = runner_mod.PACKAGED_HARDWARE_DIR.parent / "rocm" / "rocm_generic.yaml"
+    suite = tmp_path / "suite.yaml"
+    suite.write_text(yaml.safe_dump({
+        "name": "inherit", "device": {"profile": str(generic)}, "runtime": {"profile": str(runtime)},
+        "profiling": {"enabled": True, "engine": "rocprof",
+                      "params": {"binary": str(profiler), "calibrate": False, "counter_passes": [["FETCH_SIZE"]]}},
+        "outputs": {"directory": str(tmp_path / "results"), "formats": ["json"]},
+        "benchmarks": [{"benchmark": "hbm", "params": {"backend": "native", "dtypes": ["float32"],
+                                                        "modes": ["copy"], "size_mib": 1,
+                                                        "native": {"binary": str(executable)}}}],
+    }), encoding="utf-8")
+    monkeypatch.setattr(runner_mod, "load_torch", lambda: object())
+    monkeypatch.setattr(runner_mod, "detect_device",
+                        lambda torch_module, device_id=0: DeviceInfo(index=0, name="AMD Instinct MI355X"))
+    summary = run_suite(suite)
+    assert summary.profile_note and "amd-instinct-mi355x" in summary.profile_note
+    (record,) = summary.records
+    assert record.status == "ok" and record.raw_metrics["peak_bandwidth_gbps"] == 8000.0
+    assert record.metrics["hbm_efficiency_pct"] > 0
