@@ -209,7 +209,7 @@ int mb_kernel_info(int kind, int a, int b, int64_t m, int64_t n, int64_t k,
 #define MB_TUNE_STREAM_SCHEDULE 3      /* 0 grid-stride, 1 one contiguous span per block */
 #define MB_TUNE_GEMM_FORCE_GENERIC 4   /* 1: the bounds-checked generic kernel for 16-bit and fp8 */
 #define MB_TUNE_GEMM_NO_SMALL_M 5      /* 1: M <= 4 stays on the MFMA kernels */
-#define MB_TUNE_GEMM_TILED_CONFIG 6    /* 0: 256x256, 1: 128x256, 2: 128x128, 3: 64x128 tiles */
+#define MB_TUNE_GEMM_TILED_CONFIG 6    /* 0: 256x256, 1: 128x256, 2: 128x128, 3: 64x128, 4: 64x64 tiles */
 #define MB_TUNE_GEMM_SPLITS 7          /* K splits, 1..512 (taken when each split is whole stages; a K off
                                           the stage depth rounds every split up to whole stages) */
 #define MB_TUNE_GEMM_FP8_MFMA 8        /* 16 or 32: the fp8 MFMA shape on the tiled kernel */

@@ -30,7 +30,7 @@ struct KnobSpec {
 bool is_bool(int64_t v) { return v == 0 || v == 1; }
 bool is_unroll(int64_t v) { return v == 1 || v == 2 || v == 4 || v == 8; }
 bool is_threads(int64_t v) { return v >= 64 && v <= 1024 && v % 64 == 0; }
-bool is_config(int64_t v) { return v >= 0 && v <= 3; }
+bool is_config(int64_t v) { return v >= 0 && v <= 4; }
 bool is_splits(int64_t v) { return v >= 1 && v <= 512; }
 bool is_mfma(int64_t v) { return v == 16 || v == 32; }
 

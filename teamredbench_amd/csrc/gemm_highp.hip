@@ -640,7 +640,8 @@ int gemm_highp_plan(int dtype, int64_t M, int64_t N, int64_t K, const DeviceProp
     }
     const int64_t gx = (N + kHpBN - 1) / kHpBN, gy = (M + kHpBM - 1) / kHpBM;
     if (gy > 65535 || gx > INT32_MAX) {
-        set_error("fp32/fp64 GEMM: M=%lld N=%lld too large", (long long)M, (long long)N);
+        set_error("fp32/fp64 GEMM: M=%lld N=%lld too large for the register-staged kernel's grid (%s)",
+                  (long long)M, (long long)N, why);
         return MB_ERR_SHAPE;
     }
     plan->implementation = f64 ? "gfx950_mfma_f64_16x16x4" : "gfx950_mfma_f32_32x32x2";

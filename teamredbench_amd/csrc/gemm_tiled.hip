@@ -1,7 +1,7 @@
 // LDS-pipelined MFMA GEMM for gfx950: C = alpha * (A * B), A (M x K) and
 // B (K x N) row-major, fp32 accumulation, output bf16 (bf16 and fp8 e4m3 /
 // e5m2 inputs) or fp16 (fp16 inputs). Tiles of 256 x 256, 128 x 256,
-// 128 x 128 or 64 x 128. Takes shapes with A's and B's rows on 16 bytes (K
+// 128 x 128, 64 x 128 or 64 x 64. Takes shapes with A's and B's rows on 16 bytes (K
 // and N multiples of 8, of 16 for fp8), any M: the rows of a partial last M
 // tile read as zeros, and the columns of a partial last N tile read the start
 // of B's next row (zeros past B's end); neither is stored. A K that is not a
@@ -26,8 +26,10 @@
 // LDS swizzles (16-byte chunk c of a row is stored at chunk c ^ f(row)):
 //   A rows (8 chunks):          f = ((r >> 1) & 7) ^ ((r & 1) << 2)
 //   16-bit B rows (32 chunks):  f = ((k << 2) ^ (k << 1)) & 15, k = row & 3
+//   16-bit B rows (8 chunks):   f = 2k,                         k = row & 3
 //   fp8 B rows (16 chunks):     f = (2k) ^ (k >> 2),            k = row & 7
 //   fp8 B rows (8 chunks):      f = k,                          k = row & 7
+//   fp8 B rows (4 chunks):      f = (k >> 1) & 3,               k = row & 7
 // Each keeps every operand read of a wave free of bank conflicts for both 8-
 // and 16-lane LDS phases (checked exhaustively on the host).
 //
@@ -75,9 +77,20 @@ constexpr int kStageK = 64;                  // bytes of K per row per stage
 constexpr int kPreBarrierMfma = 2;
 
 __device__ __forceinline__ int swz_b16(int k) { return ((k << 2) ^ (k << 1)) & 15; }
-// fp8 B rows of 256 bytes (256 columns) and of 128 bytes (128 columns).
+// 16-bit B rows of 128 bytes (64 columns, 8 chunks).
+__device__ __forceinline__ int swz_b16_128(int k) { return 2 * k; }
+// fp8 B rows of 256 bytes (256 columns), of 128 bytes (128 columns) and of 64 bytes (64 columns).
 __device__ __forceinline__ int swz_b8(int k) { return (2 * k) ^ (k >> 2); }
 __device__ __forceinline__ int swz_b8_128(int k) { return k; }
+__device__ __forceinline__ int swz_b8_64(int k) { return (k >> 1) & 3; }
+
+// The B-row swizzle of a tile's row width (bytes) and element size: chunk c of
+// B row k sits at chunk c ^ b_swizzle(k).
+template <int E, int ROW>
+__device__ __forceinline__ int b_swizzle(int k) {
+    if constexpr (E == 2) return ROW == 128 ? swz_b16_128(k & 3) : swz_b16(k & 3);
+    else return ROW == 256 ? swz_b8(k & 7) : ROW == 128 ? swz_b8_128(k & 7) : swz_b8_64(k & 7);
+}
 
 typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x4_t __attribute__((__vector_size__(4 * sizeof(__bf16))));
@@ -239,7 +252,7 @@ __device__ __forceinline__ u32x2 read_b_piece(const unsigned char* st, int nb, i
         constexpr int row_bytes = BN * 2;
         const int k = 16 * s + 8 * (g >> 1) + 4 * t + (i >> 2);
         const int n = nb + 16 * (g & 1) + 4 * (i & 3);
-        const int off = k * row_bytes + (((n >> 3) ^ swz_b16(k & 3)) << 4) + 8 * (i & 1);
+        const int off = k * row_bytes + (((n >> 3) ^ b_swizzle<2, row_bytes>(k)) << 4) + 8 * (i & 1);
         const bf16x4_t v =
             __builtin_amdgcn_ds_read_tr16_b64_v4bf16((MB_LDS bf16x4_t*)((MB_LDS unsigned char*)st + off));
         return __builtin_bit_cast(u32x2, v);
@@ -247,7 +260,7 @@ __device__ __forceinline__ u32x2 read_b_piece(const unsigned char* st, int nb, i
         constexpr int row_bytes = BN;
         const int k = 32 * (g >> 1) + 8 * t + (i >> 1);
         const int n = nb + 16 * (g & 1) + 8 * (i & 1);
-        const int f = row_bytes == 256 ? swz_b8(k & 7) : swz_b8_128(k & 7);
+        const int f = b_swizzle<1, row_bytes>(k);
         const int off = k * row_bytes + (((n >> 4) ^ f) << 4) + 8 * (i & 1);
         const i32x2_t v = __builtin_amdgcn_ds_read_tr8_b64_v2i32((MB_LDS i32x2_t*)((MB_LDS unsigned char*)st + off));
         return __builtin_bit_cast(u32x2, v);
@@ -268,8 +281,8 @@ __device__ __forceinline__ u32x2 pack4(float a, float b, float c, float d) {
 
 // Second half of the epilogue: a wave's (WTM x ROW_BYTES / 2) tile, staged in
 // LDS as 16-bit values (chunk c of row r at chunk c ^ (r % chunks)), read back
-// row by row and stored so that 16 (8) lanes write one 256-byte (128-byte) C
-// row segment: whole cache lines. Read-backs go out in batches of BATCH
+// row by row and stored so that 16 (8, 4) lanes write one 256-byte (128-,
+// 64-byte) C row segment: whole cache lines, half lines for 64 bytes. Read-backs go out in batches of BATCH
 // before their stores, so no store waits on the LDS read just before it.
 // The stores are nontemporal: nothing in the kernel reads C back, and every
 // CU stores its tile at about the same moment, so keeping those lines out of
@@ -328,8 +341,8 @@ gemm_tiled_kernel(const unsigned char* __restrict__ A, const unsigned char* __re
     constexpr int LDS_BYTES = NA * PAIR + NB * B_BYTES;
     static_assert(PAIR % (1024 * W) == 0 && B_BYTES % (1024 * W) == 0, "stage must split over the waves");
     static_assert(A_INSTR % 2 == 0, "A offsets assume an even number of pair loads per wave");
-    static_assert(B_ROW == 512 || B_ROW == 256 || (E == 1 && B_ROW == 128),
-                  "B swizzles cover 16-bit rows of 512 / 256 bytes and fp8 rows of 256 / 128 bytes");
+    static_assert(E == 2 ? (B_ROW == 512 || B_ROW == 256 || B_ROW == 128) : (B_ROW == 256 || B_ROW == 128 || B_ROW == 64),
+                  "B swizzles cover 16-bit rows of 512 / 256 / 128 bytes and fp8 rows of 256 / 128 / 64 bytes");
     static_assert(WTM % 32 == 0 && WTN % 32 == 0, "wave tile must be 32-aligned");
     static_assert(NA >= 2 && NB >= 3 && LDS_BYTES <= 160 * 1024, "LDS ring does not fit");
     constexpr LoadSchedule kSched = load_schedule(NA, NB, A_INSTR, B_INSTR);
@@ -393,7 +406,7 @@ gemm_tiled_kernel(const unsigned char* __restrict__ A, const unsigned char* __re
     for (int q = 0; q < B_INSTR; ++q) {
         const int lin = (wave * B_INSTR + q) * 1024 + lane * 16;   // LDS byte in the B part
         const int row = lin / B_ROW, pchunk = (lin % B_ROW) >> 4;
-        const int f = E == 2 ? swz_b16(row & 3) : B_ROW == 256 ? swz_b8(row & 7) : swz_b8_128(row & 7);
+        const int f = b_swizzle<E, B_ROW>(row);
         b_voff[q] = row * ldb + ((pchunk ^ f) << 4);
     }
 
@@ -584,10 +597,11 @@ gemm_tiled_kernel(const unsigned char* __restrict__ A, const unsigned char* __re
     // from registers, every store instruction would put 16 bytes into each of
     // 32 rows. Instead each wave rounds its (WTM x WTN) tile to 16 bits into
     // its own region of the LDS ring (all of it is free after the final wait
-    // and barrier), then reads it back row by row so that 16 (8) lanes store
-    // one 256-byte (128-byte) row segment of a 128- (64-) column wave tile:
-    // whole cache lines, half the store instructions. Staged rows are 16 (8)
-    // chunks of 16 bytes; chunk c of row r sits at chunk c ^ (r % chunks),
+    // and barrier), then reads it back row by row so that 16 (8, 4) lanes
+    // store one 256-byte (128-, 64-byte) row segment of a 128- (64-, 32-)
+    // column wave tile: whole cache lines (half lines for 32 columns), half
+    // the store instructions. Staged rows are 16 (8, 4) chunks of 16 bytes;
+    // chunk c of row r sits at chunk c ^ (r % chunks),
     // which keeps the reads (all chunks of a few rows) free of bank conflicts;
     // the writes (one chunk of 32 rows) conflict 2-way, since each half wave
     // fills only one 8-byte half of every chunk. Rows at or past M (a
@@ -600,7 +614,8 @@ gemm_tiled_kernel(const unsigned char* __restrict__ A, const unsigned char* __re
     if (BM > 128 || ws == nullptr) {
         constexpr int ROW_BYTES = WTN * 2;
         constexpr int ROW_CHUNKS = ROW_BYTES / 16;
-        static_assert(ROW_CHUNKS == 16 || ROW_CHUNKS == 8, "staging covers wave tiles 128 or 64 columns wide");
+        static_assert(ROW_CHUNKS == 16 || ROW_CHUNKS == 8 || ROW_CHUNKS == 4,
+                      "staging covers wave tiles 128, 64 or 32 columns wide");
         static_assert(W * WTM * ROW_BYTES <= LDS_BYTES, "the waves' tiles must fit the LDS ring");
         unsigned char* stage = lds + wave * WTM * ROW_BYTES;
         // alpha is 1 except for scaled fp8: the unscaled instantiation skips
@@ -1021,6 +1036,7 @@ constexpr TiledConfig kConfigs[] = {
     {128, 256, 2, 2, 3, 6, 8},  // 1: mid-size problems, 64 x 128 per wave; 3 x 16 + 6 x 16 KiB
     {128, 128, 2, 2, 3, 6, 4},  // 2: few tiles, N % 256 != 0: 64 x 64 per wave; 3 x 16 + 6 x 8 KiB
     {64, 128, 2, 2, 3, 6, 4},   // 3: small and skinny problems: 32 x 64 per wave; 3 x 8 + 6 x 8 KiB
+    {64, 64, 2, 2, 3, 6, 4},    // 4: one-round problems of up to 256 such tiles: 32 x 32 per wave; 3 x 8 + 6 x 4 KiB
 };
 
 template <int DT, int CFG>
@@ -1048,9 +1064,11 @@ int launch_cfg(const void* A, const void* B, void* C, int64_t M, int64_t N, int6
     auto pick = [&](auto rk) -> Kernel {
         constexpr bool RK = decltype(rk)::value;
         if constexpr (is_fp8(DT)) {
-            if (plan.frag_m == 16)
-                return scaled ? gemm_fp8_mi16_kernel<DT, c.bm, c.bn, c.wgm, c.wgn, c.na, c.nb, true, RK>
-                              : gemm_fp8_mi16_kernel<DT, c.bm, c.bn, c.wgm, c.wgn, c.na, c.nb, false, RK>;
+            if constexpr (c.bn >= 128) {   // the 16x16x128 kernel's B swizzles cover rows of 128 bytes or more
+                if (plan.frag_m == 16)
+                    return scaled ? gemm_fp8_mi16_kernel<DT, c.bm, c.bn, c.wgm, c.wgn, c.na, c.nb, true, RK>
+                                  : gemm_fp8_mi16_kernel<DT, c.bm, c.bn, c.wgm, c.wgn, c.na, c.nb, false, RK>;
+            }
             if (scaled) return gemm_tiled_kernel<DT, c.bm, c.bn, c.wgm, c.wgn, c.na, c.nb, true, RK>;
         }
         return gemm_tiled_kernel<DT, c.bm, c.bn, c.wgm, c.wgn, c.na, c.nb, false, RK>;
@@ -1077,6 +1095,7 @@ int launch_dtype(const GemmPlan& plan, const void* A, const void* B, void* C, in
     if (plan.config == 0) return launch_cfg<DT, 0>(A, B, C, M, N, K, alpha, plan, workspace, stream);
     if (plan.config == 2) return launch_cfg<DT, 2>(A, B, C, M, N, K, alpha, plan, workspace, stream);
     if (plan.config == 3) return launch_cfg<DT, 3>(A, B, C, M, N, K, alpha, plan, workspace, stream);
+    if (plan.config == 4) return launch_cfg<DT, 4>(A, B, C, M, N, K, alpha, plan, workspace, stream);
     return launch_cfg<DT, 1>(A, B, C, M, N, K, alpha, plan, workspace, stream);
 }
 
@@ -1176,7 +1195,8 @@ int gemm_tiled_plan(int dtype, int64_t M, int64_t N, int64_t K, const DeviceProp
     // against 49.4 at 2.
     int splits = 1;
     if (!fill_rule && (cfg < 0 || kConfigs[cfg].bm <= 128)) {
-        constexpr double kRate[4] = {0.0, 3.70e12, 2.87e12, 1.99e12}, kBw = 6.26e12, kRound = 2.71e-6,
+        // kRate[4] (64 x 64 tiles) only prices the split count when that configuration is forced.
+        constexpr double kRate[5] = {0.0, 3.70e12, 2.87e12, 1.99e12, 1.20e12}, kBw = 6.26e12, kRound = 2.71e-6,
                          kReduce = 4.72e-6;
         int cands[3] = {1, 2, 3}, n_cands = 3, first = 0;
         if (cfg >= 0) cands[0] = cfg, n_cands = 1;
@@ -1203,6 +1223,23 @@ int gemm_tiled_plan(int dtype, int64_t M, int64_t N, int64_t K, const DeviceProp
             }
         }
     }
+    // 64 x 64 tiles for narrow problems: a plan of 64 x 128 tiles with N at
+    // most 2048 takes them with half its K splits (the same block count, each
+    // block half the columns over twice the K: one reduction pass less, or
+    // none), or, unsplit, when twice its blocks still fit one round. On
+    // MI355X, B from HBM, 61 such shapes (M 8..1024, N 256..2048, K
+    // 512..16384, bf16 and fp8 e4m3) ran 1.128x faster in geometric mean
+    // (0.96x - 1.33x): 1024^3 bf16 6.3 against 7.6 us, 1024 x 1024 x 2048 7.8
+    // against 14.0 (no split instead of two), 128 x 1024 x 8192 12.8 against
+    // 14.6. Wider N keeps 64 x 128 tiles: their 256-byte B rows stream HBM
+    // better (16 x 8192 x 8192 fp8 19.7 against 22.1 us on 64 x 64).
+    if (pinned < 0 && cfg == 3 && N <= 2048) {
+        const int s4 = splits > 1 ? splits / 2 : 1;
+        if (splits > 1 || tiles(4) <= cus) {
+            cfg = 4;
+            splits = s4;
+        }
+    }
     const int64_t force_splits = tuning(MB_TUNE_GEMM_SPLITS);
     if (force_splits >= 1 && split_ok(force_splits)) splits = (int)force_splits;
     if (kConfigs[cfg].bm > 128) splits = 1;   // the 256-row kernels carry no split path
@@ -1221,7 +1258,7 @@ int gemm_tiled_plan(int dtype, int64_t M, int64_t N, int64_t K, const DeviceProp
     // within 0.6% either way there. The gemm_fp8_mfma override (16 or 32)
     // forces either.
     const int64_t mfma_force = tuning(MB_TUNE_GEMM_FP8_MFMA);
-    const bool mi16 = e == 1 && (split_k_len(splits) / stage_k) % 2 == 0 &&
+    const bool mi16 = e == 1 && (split_k_len(splits) / stage_k) % 2 == 0 && c.bn >= 128 &&
                       (mfma_force == 16 || (mfma_force != 32 && c.bm >= 128));
     const int frag = mi16 ? 16 : 32;
     plan->implementation = mi16 ? "gfx950_mfma16_lds_dma" : "gfx950_mfma32_lds_dma";

@@ -80,7 +80,7 @@ def test_tuning_knobs_validate_and_restore_without_a_gpu():
         assert lib.get_tuning("gemm_splits") == 4 and lib.get_tuning("stream_unroll") == 8
     assert lib.get_tuning("gemm_splits") is None and lib.get_tuning("stream_unroll") is None
     for name, bad in (("stream_unroll", 3), ("stream_threads", 96), ("stream_threads", 2048),
-                      ("gemm_tiled_config", 4), ("gemm_splits", 0), ("gemm_splits", 513), ("gemm_fp8_mfma", 8),
+                      ("gemm_tiled_config", 5), ("gemm_splits", 0), ("gemm_splits", 513), ("gemm_fp8_mfma", 8),
                       ("gemm_force_generic", 2)):
         with pytest.raises(capi.NativeLibraryError, match="cannot take") as err:
             lib.set_tuning(name, bad)

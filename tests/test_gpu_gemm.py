@@ -86,7 +86,7 @@ def test_gemm_random_matches_fp32_matmul(lib, dtype, shape):
 
 
 @pytest.mark.parametrize("dtype", LOWP)
-@pytest.mark.parametrize("config", ["0", "1", "2", "3"])
+@pytest.mark.parametrize("config", ["0", "1", "2", "3", "4"])
 @pytest.mark.parametrize("shape", [(256, 256, 128), (256, 512, 64), (256, 512, 1024), (512, 256, 4096), (768, 1280, 384)])
 def test_tiled_configurations(lib, dtype, config, shape, tune):
     # Every tiled configuration on shapes it divides, selected through the
@@ -95,13 +95,14 @@ def test_tiled_configurations(lib, dtype, config, shape, tune):
     m, n, k = shape
     info = lib.gemm_info(capi.DTYPES[dtype], m, n, k)
     assert info["implementation"] == tiled_impl(dtype, k, info)
-    assert (info["tile_m"], info["tile_n"]) == {"0": (256, 256), "1": (128, 256), "2": (128, 128), "3": (64, 128)}[config]
+    assert (info["tile_m"], info["tile_n"]) == {"0": (256, 256), "1": (128, 256), "2": (128, 128), "3": (64, 128),
+                                                "4": (64, 64)}[config]
     print(f"[gemm] tiled cfg {config} {dtype} {shape}", flush=True)
     _check_random(lib, dtype, m, n, k, seed=k)
 
 
 @pytest.mark.parametrize("dtype", ["bfloat16", "float8_e4m3fn"])
-@pytest.mark.parametrize("config", ["0", "1", "2", "3"])
+@pytest.mark.parametrize("config", ["0", "1", "2", "3", "4"])
 @pytest.mark.parametrize("ksteps", [1, 2, 3, 4, 5, 6, 7, 8, 9, 11, 12, 13, 25, 37])
 def test_tiled_stage_counts(lib, dtype, config, ksteps, tune):
     # A is loaded two 64-byte K stages at a time: odd stage counts leave the
@@ -133,28 +134,48 @@ def test_forced_splits_with_odd_stage_counts(lib, dtype, splits, ksteps, tune):
 
 @pytest.mark.parametrize("dtype", LOWP)
 @pytest.mark.parametrize("shape", [(512, 384, 256), (1000, 1152, 320), (64, 640, 512), (16, 1152, 4096), (3, 128, 64)])
-def test_n_multiple_of_128_takes_128x128_tiles(lib, dtype, shape, tune):
-    # Shapes with N a multiple of 128 but not 256 run the pipelined kernel on 128 x 128 tiles
-    # (ragged M through the buffer range checks, skinny shapes with K splits).
+def test_n_multiple_of_128_takes_128_or_64_column_tiles(lib, dtype, shape, tune):
+    # Shapes with N a multiple of 128 but not 256 run the pipelined kernel on 128-column tiles, or, N being
+    # at most 2048 here, 64 x 64 tiles where the plan would take 64 x 128 (ragged M through the buffer range
+    # checks, skinny shapes with K splits).
     tune(gemm_no_small_m=1)  # keep M <= 4 on the tiled kernel too
     m, n, k = shape
     info = lib.gemm_info(capi.DTYPES[dtype], m, n, k)
-    assert info["implementation"] == tiled_impl(dtype, k, info) and info["tile_n"] == 128 and info["tile_m"] in (64, 128)
+    assert info["implementation"] == tiled_impl(dtype, k, info)
+    assert (info["tile_m"], info["tile_n"]) in ((128, 128), (64, 128), (64, 64)), info
     print(f"[gemm] n%128 {dtype} {shape} split {info['split_k']}", flush=True)
     _check_random(lib, dtype, m, n, k, seed=n + 3)
 
 
 @pytest.mark.parametrize("dtype", ["bfloat16", "float16"])
-@pytest.mark.parametrize("shape, tile_m", [((2048, 2048, 2048), 128), ((1024, 1024, 1024), 64), ((640, 1536, 768), 64)])
-def test_few_tiles_take_128x128_tiles(lib, dtype, shape, tile_m):
-    # Several tile rows that would leave half the CUs idle on 128 x 256 tiles
-    # run 128 x 128 tiles, unsplit (the default plan, not an override); the
-    # smallest of them 64 x 128 tiles, which the cost model rates faster there.
+@pytest.mark.parametrize("shape, tile", [((2048, 2048, 2048), (128, 128)), ((1024, 1024, 1024), (64, 64)),
+                                         ((640, 1536, 768), (64, 64)), ((1024, 2048, 1024), (64, 128))])
+def test_few_tiles_take_smaller_tiles(lib, dtype, shape, tile):
+    # Several tile rows that would leave half the CUs idle on 128 x 256 tiles run 128 x 128 tiles, unsplit
+    # (the default plan, not an override); the smaller ones 64 x 128 tiles, which the cost model rates faster
+    # there, and with N at most 2048 64 x 64 tiles where twice the blocks still fit one round (1024^3 bf16
+    # 6.3 against 7.6 us, 640 x 1536 x 768 5.8 against 6.9) -- 1024 x 2048 x 1024 would need two.
     m, n, k = shape
     info = lib.gemm_info(capi.DTYPES[dtype], m, n, k)
-    assert (info["tile_m"], info["tile_n"], info["split_k"]) == (tile_m, 128, 1)
-    print(f"[gemm] 128x128 default {dtype} {shape}", flush=True)
+    assert (info["tile_m"], info["tile_n"], info["split_k"]) == (*tile, 1)
+    print(f"[gemm] few tiles {dtype} {shape} -> {tile}", flush=True)
     _check_random(lib, dtype, m, n, k, seed=n)
+
+
+@pytest.mark.parametrize("dtype, shape, splits", [
+    ("bfloat16", (1024, 1024, 1024), 1), ("float8_e4m3fn", (1024, 1024, 1024), 1),
+    ("bfloat16", (1024, 1024, 2048), 1), ("float8_e4m3fn", (1024, 1024, 2048), 1),
+    ("bfloat16", (512, 256, 4096), 8), ("float8_e4m3fn", (512, 256, 4096), 4),
+    ("bfloat16", (128, 1024, 8192), 8), ("float8_e4m3fn", (128, 1024, 8192), 8),
+    ("bfloat16", (100, 2048, 4096), 4), ("float8_e4m3fn", (100, 2048, 4096), 4)])
+def test_narrow_split_plans_take_64x64_tiles_with_half_the_splits(lib, dtype, shape, splits):
+    # N <= 2048 on 64 x 128 tiles with K splits: 64 x 64 tiles at half the splits, the same block count
+    # (1024 x 1024 x 2048 bf16 7.8 us unsplit against 14.0 at two splits of 64 x 128 tiles; 512 x 256 x 4096
+    # 8.9 against 11.8; 128 x 1024 x 8192 12.8 against 14.6).
+    m, n, k = shape
+    info = lib.gemm_info(capi.DTYPES[dtype], m, n, k)
+    assert (info["tile_m"], info["tile_n"], info["split_k"]) == (64, 64, splits), info
+    _check_random(lib, dtype, m, n, k, seed=m + n)
 
 
 @pytest.mark.parametrize("dtype, shape, tile_m", [("bfloat16", (16, 8192, 8192), 64), ("float16", (16, 8192, 8192), 64),
@@ -630,7 +651,7 @@ def test_overrides_are_reported_and_the_environment_is_ignored(lib, tune, monkey
     assert forced["split_k"] == 3 and forced["overrides"] == {"gemm_splits": 3}
     assert lib.stream_info(capi.OP_TRIAD, capi.DT_FLOAT32, 1 << 20)["overrides"] == {}
     with pytest.raises(capi.NativeLibraryError) as err:
-        lib.set_tuning("gemm_tiled_config", 4)
+        lib.set_tuning("gemm_tiled_config", 5)
     assert err.value.status == capi.MB_ERR_INVALID_ARG
 
 
@@ -655,9 +676,16 @@ def test_kernel_info_names_the_fallback(lib, dtype, shape, impl, reason):
 
 @pytest.mark.parametrize("dtype, shape", [("float32", (1 << 31, 4, 4)), ("float64", (1 << 31, 2, 2)),
                                           ("float32", ((1 << 31) + 256, 256, 16))])
-def test_highp_rows_past_int32_take_the_register_staged_kernel(lib, dtype, shape):
-    # Plan only, nothing launched: the LDS-DMA kernels index rows with int, so M >= 2^31 must fall back
-    # to the register-staged kernel (int64 indexes) and say why.
-    info = lib.gemm_info(capi.DTYPES[dtype], *shape)
-    assert not info["implementation"].endswith("lds_dma"), info
-    assert "2^31" in info["fallback"], info
+def test_highp_rows_past_int32_are_refused(lib, dtype, shape):
+    # Plan only, nothing launched: the LDS-DMA kernels index rows with int and the register-staged kernel's
+    # grid covers at most 65535 row blocks, so M >= 2^31 is refused with the reason, never planned onto a
+    # kernel whose row guard would skip every store.
+    with pytest.raises(capi.NativeLibraryError) as err:
+        lib.gemm_info(capi.DTYPES[dtype], *shape)
+    assert err.value.status == capi.MB_ERR_SHAPE and "2^31" in str(err.value)
+
+
+def test_highp_rows_beyond_the_staged_grid_take_the_lds_dma_kernel(lib):
+    # 2^24 rows: past the register-staged kernel's 65535 row blocks, within the LDS-DMA kernels' int rows.
+    info = lib.gemm_info(capi.DT_FLOAT32, 1 << 24, 256, 16)
+    assert info["implementation"].endswith("lds_dma") and info["fallback"] == "", info

@@ -31,6 +31,16 @@ def swz_b16(k: int) -> int:
     return ((k << 2) ^ (k << 1)) & 15
 
 
+def swz_b16_128(k: int) -> int:
+    """16-bit B rows of 128 bytes (64 columns)."""
+    return 2 * k
+
+
+def swz_b8_64(k: int) -> int:
+    """fp8 B rows of 64 bytes (64 columns)."""
+    return (k >> 1) & 3
+
+
 def swz_b8(k: int) -> int:
     return (2 * k) ^ (k >> 2)
 
@@ -75,12 +85,13 @@ def test_a_swizzle_is_a_permutation_per_row():
 
 
 def b_tr16_addrs(row_bytes: int, nb: int, s: int, t: int) -> list[int]:
+    swz = swz_b16_128 if row_bytes == 128 else swz_b16
     out = []
     for lane in range(64):
         g, i = lane >> 4, lane & 15
         k = 16 * s + 8 * (g >> 1) + 4 * t + (i >> 2)
         n = nb + 16 * (g & 1) + 4 * (i & 3)
-        out.append(k * row_bytes + (((n >> 3) ^ swz_b16(k & 3)) << 4) + 8 * (i & 1))
+        out.append(k * row_bytes + (((n >> 3) ^ swz(k & 3)) << 4) + 8 * (i & 1))
     return out
 
 
@@ -90,20 +101,21 @@ def b_tr8_addrs(nb: int, t: int, row_bytes: int = 256) -> list[int]:
         g, i = lane >> 4, lane & 15
         k = 32 * (g >> 1) + 8 * t + (i >> 1)
         n = nb + 16 * (g & 1) + 8 * (i & 1)
-        f = swz_b8(k & 7) if row_bytes == 256 else k & 7  # 128-byte rows (128 columns): f = k
+        # 128-byte rows (128 columns): f = k; 64-byte rows (64 columns): swz_b8_64
+        f = swz_b8(k & 7) if row_bytes == 256 else (k & 7) if row_bytes == 128 else swz_b8_64(k & 7)
         out.append(k * row_bytes + (((n >> 4) ^ f) << 4) + 8 * (i & 1))
     return out
 
 
 def test_b_transposing_reads_are_conflict_free():
-    for row_bytes, bn in ((512, 256), (256, 128)):
+    for row_bytes, bn in ((512, 256), (256, 128), (128, 64)):
         for nb in range(0, bn, 32):
             for s in range(2):
                 for t in range(2):
                     addrs = b_tr16_addrs(row_bytes, nb, s, t)
                     assert worst_lanes_per_bank(addrs, 8, 16, 32) == 1
                     assert worst_lanes_per_bank(addrs, 8, 32, 64) == 1
-    for row_bytes in (256, 128):
+    for row_bytes in (256, 128, 64):
         for nb in range(0, row_bytes, 32):
             for t in range(4):
                 addrs = b_tr8_addrs(nb, t, row_bytes)
@@ -111,7 +123,7 @@ def test_b_transposing_reads_are_conflict_free():
                 assert worst_lanes_per_bank(addrs, 8, 32, 64) == 1
 
 
-@pytest.mark.parametrize("bm, waves", [(256, 4), (128, 4), (64, 4)])
+@pytest.mark.parametrize("bm, waves", [(256, 4), (128, 4), (64, 4)])   # 64 rows: the 64 x 128 and 64 x 64 tiles
 @pytest.mark.parametrize("lda", [128, 8192, 16384 + 128])  # A row bytes, multiples of 128
 def test_a_loads_cover_whole_lines_and_split_offsets(bm, waves, lda):
     pair_bytes = 2 * bm * STAGE
@@ -206,8 +218,8 @@ def simulate_ring(na: int, nb: int, ai: int, bi: int, ksteps: int,
 
 
 # (A pair slots, B stage slots, A loads per wave per pair, B loads per wave per stage) of the
-# four tiled configurations: 256x256 (16-bit and fp8), 128x256, 128x128 and 64x128 (16-bit).
-CONFIGS = [(3, 4, 8, 4), (3, 6, 4, 4), (3, 6, 4, 2), (3, 6, 2, 2)]
+# five tiled configurations: 256x256 (16-bit and fp8), 128x256, 128x128, 64x128 and 64x64 (16-bit).
+CONFIGS = [(3, 4, 8, 4), (3, 6, 4, 4), (3, 6, 4, 2), (3, 6, 2, 2), (3, 6, 2, 1)]
 
 
 @pytest.mark.parametrize("cfg", CONFIGS)
@@ -222,6 +234,7 @@ def test_ring_waits_of_the_configurations():
     assert load_schedule(3, 6, 4, 4) == (28, 20, 24)
     assert load_schedule(3, 6, 4, 2) == (18, 12, 16)
     assert load_schedule(3, 6, 2, 2) == (14, 10, 12)
+    assert load_schedule(3, 6, 2, 1) == (9, 6, 8)
 
 
 @pytest.mark.parametrize("loosen", [(1, 0, 0), (0, 1, 0), (0, 0, 1)])
@@ -489,3 +502,11 @@ def test_mi16_simulation_catches_a_wait_one_load_too_loose(loosen, split_a):
     waits = (prologue + loosen[0], odd + loosen[1], even + loosen[2])
     with pytest.raises(AssertionError):
         simulate_ring_mi16(3, 4, 8, 4, 16, waits, split_a=split_a)
+
+
+def test_b_swizzles_of_narrow_rows_permute_within_the_row():
+    # chunk c of B row k sits at chunk c ^ f(k): f must keep every chunk inside its row
+    for k in range(4):
+        assert sorted(c ^ swz_b16_128(k) for c in range(8)) == list(range(8))      # 128-byte 16-bit rows
+    for k in range(8):
+        assert sorted(c ^ swz_b8_64(k) for c in range(4)) == list(range(4))        # 64-byte fp8 rows
