@@ -22,13 +22,16 @@ in HBM. The printed JSON line carries:
                        a 512-row slab of the same problem (bf16 operands for
                        bf16; for fp8, whose torch.mm has no CPU kernel, the
                        dequantised fp32 operands the oracle multiplies);
+  mfma_ceiling         the sustained TFLOP/s of the MFMA instructions those
+                       GEMMs run, with no memory traffic, in the same process
+                       (each GEMM's frac_of_mfma_ceiling divides by it);
   cpu_baseline         the reference torch op (torch.add(b, c, alpha=3.0,
                        out=a)) on CPU tensors on this host's cores: the CPU
                        triad configuration (2^24 elements, seed 0, 5 warmup +
                        20 timed), plus the same op at the GPU step's size.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-gemm]
-                       [--cpu-iterations I] [--no-cpu]
+                       [--no-mfma-ceiling] [--cpu-iterations I] [--no-cpu]
 """
 from __future__ import annotations
 
@@ -188,6 +191,55 @@ def bench_gemm(torch, lib, capi, dtype: str, size: int, warmup: int, iterations:
     }
 
 
+CEILING_INSTRUCTIONS = ("v_mfma_f32_32x32x16_bf16", "v_mfma_scale_f32_16x16x128_f8f6f4",
+                        "v_mfma_scale_f32_32x32x64_f8f6f4")
+# The instruction each 8192^3 GEMM kernel runs: its sustained rate bounds what the GEMM's MFMA work can reach.
+GEMM_INSTRUCTION = {"bfloat16": "v_mfma_f32_32x32x16_bf16", "float8_e4m3fn": "v_mfma_scale_f32_16x16x128_f8f6f4"}
+
+
+def bench_mfma_ceiling(torch, lib, capi, names=CEILING_INSTRUCTIONS, launch_s: float = 2e-3,
+                       warmup_s: float = GEMM_WARMUP_S, launches: int = 20) -> dict:
+    """Sustained TFLOP/s of each MFMA instruction with no memory traffic (mb_mfma_ceiling): one 256-thread
+    block per CU issuing 8 independent MFMAs per wave per round on random operands of the instruction's type,
+    about launch_s per launch, an untimed warmup of warmup_s (the clock settles under the power limit), then
+    `launches` event-timed launches bracketed by clock stamps."""
+    from teamredbench_amd.profiling.clock import ClockWindow
+
+    dev = torch.device("cuda:0")
+    handle = torch.cuda.current_stream(dev).cuda_stream
+    blocks = torch.cuda.get_device_properties(0).multi_processor_count
+    out = torch.empty(256 * blocks, device=dev, dtype=torch.float32)
+    gen = torch.Generator().manual_seed(0)
+    result = {}
+    for name in names:
+        code, flop, dtype = capi.MFMA_INSTRUCTIONS[name]
+        values = torch.randn(capi.MFMA_CEILING_OPERAND_BYTES, generator=gen)
+        if dtype == "bfloat16":
+            raw = values[: capi.MFMA_CEILING_OPERAND_BYTES // 2].to(torch.bfloat16).view(torch.uint8)
+        elif dtype == "float8_e4m3fn":
+            raw = values.to(torch.float8_e4m3fn).view(torch.uint8)
+        else:
+            raw = values[: capi.MFMA_CEILING_OPERAND_BYTES // 4].view(torch.uint8)
+        ops = raw.to(dev)
+        per_round = blocks * 4 * capi.MFMA_CEILING_CHAINS * flop
+        probe = lib.mfma_ceiling(code, ops.data_ptr(), out.data_ptr(), blocks, 256, 1, 2, handle)
+        iterations = max(2, int(launch_s / probe * 256))
+        per_launch = lib.mfma_ceiling(code, ops.data_ptr(), out.data_ptr(), blocks, iterations, 0, 1, handle)
+        warmup = max(1, int(warmup_s / per_launch))
+        lib.mfma_ceiling(code, ops.data_ptr(), out.data_ptr(), blocks, iterations, warmup, 1, handle)
+        clock = ClockWindow(torch, lib, handle)
+        clock.start()
+        secs = lib.mfma_ceiling(code, ops.data_ptr(), out.data_ptr(), blocks, iterations, 0, launches, handle)
+        clock.stop()
+        torch.cuda.synchronize()
+        rounds = (iterations + 1) // 2 * 2
+        tflops = per_round * rounds / secs / 1e12
+        result[name] = {"tflops": round(tflops, 1), "peak": MFMA_PEAK_TFLOPS.get(dtype, 157.3),
+                        "frac_of_peak": round(tflops / MFMA_PEAK_TFLOPS.get(dtype, 157.3), 4),
+                        "launch_us": round(secs * 1e6, 1), "clock": clock.summary()}
+    return result
+
+
 def _cpu_quota() -> float | None:
     """CPUs the cgroup quota allows this process (cpu.max), or None when unlimited or unreadable."""
     try:
@@ -292,6 +344,8 @@ def main() -> int:
                         help="timed CPU iterations at the GPU step's 2^28 size, beside the 2^24 CPU triad "
                              "configuration (0 = that configuration only); --no-cpu skips the CPU baseline")
     parser.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    parser.add_argument("--no-mfma-ceiling", action="store_true",
+                        help="skip the sustained-rate measurement of the MFMA instructions the GEMMs run")
     parser.add_argument("--calibration-copy", action="store_true",
                         help="before the triad, launch the fp32 copy kernel 3 times over 2^28 elements (1 GiB read, "
                              "1 GiB written per launch, untimed): the known traffic that scales FETCH_SIZE / "
@@ -339,6 +393,16 @@ def main() -> int:
             gemm[dtype] = bench_gemm(torch, lib, capi, dtype, 8192, warmup=3, iterations=args.gemm_iterations)
             _log(f"gemm {dtype}: {gemm[dtype]['achieved_tflops']:.1f} TFLOPS ({gemm[dtype]['mfu_pct']:.1f}% MFU)")
 
+    ceiling = None
+    if not args.no_gemm and not args.no_mfma_ceiling:
+        _log("mfma ceiling: " + ", ".join(CEILING_INSTRUCTIONS))
+        ceiling = bench_mfma_ceiling(torch, lib, capi)
+        for dtype, entry in gemm.items():
+            top = ceiling[GEMM_INSTRUCTION[dtype]]["tflops"]
+            entry["mfma_instruction"] = GEMM_INSTRUCTION[dtype]
+            entry["frac_of_mfma_ceiling"] = round(entry["achieved_tflops"] / top, 4)
+        _log("mfma ceiling: " + ", ".join(f"{k} {v['tflops']} TFLOPS" for k, v in ceiling.items()))
+
     baseline = None
     if not args.no_cpu:
         _log("cpu baseline: 2^24 fp32 triad, 5 warmup + 20 timed")
@@ -385,6 +449,7 @@ def main() -> int:
         "parity": triad["parity"],
         "kernel_info": triad["info"],
         "gemm": gemm or None,
+        "mfma_ceiling": ceiling,
         "cpu_baseline": baseline,
     }
     if traffic:

@@ -245,6 +245,28 @@ int64_t mb_get_tuning(int knob);
 #define MB_CLOCK_REALTIME_HZ 100000000
 int mb_clock_stamp(uint64_t* out, void* stream);
 
+/*
+ * MFMA ceiling. No counterpart in the reference: a measurement aid that
+ * gives the rate one MFMA instruction sustains on this part with no memory
+ * traffic, under the same power limit a GEMM runs under. `blocks` blocks of
+ * 256 threads (one per CU fills the part, one wave per SIMD) each run
+ * `iterations` rounds of 8 independent MFMAs per wave, alternating between
+ * two operand sets read from `operands` (MB_MFMA_CEILING_OPERAND_BYTES of
+ * device memory holding values of the instruction's input type; 128 bytes
+ * per lane), and write one float per thread to `out` (device memory for
+ * 256 * blocks floats). `warmup` untimed launches, then `launches` timed on
+ * `stream` between two events; *elapsed_s = seconds per launch. One launch
+ * does blocks * 4 * iterations * 8 MFMAs (iterations rounded up to even).
+ */
+#define MB_MFMA_BF16_32X32X16 0   /* v_mfma_f32_32x32x16_bf16:          32768 FLOP per wave instruction */
+#define MB_MFMA_BF16_16X16X32 1   /* v_mfma_f32_16x16x32_bf16:          16384 */
+#define MB_MFMA_FP8_32X32X64 2    /* v_mfma_scale_f32_32x32x64_f8f6f4:  131072 */
+#define MB_MFMA_FP8_16X16X128 3   /* v_mfma_scale_f32_16x16x128_f8f6f4: 65536 */
+#define MB_MFMA_F32_32X32X2 4     /* v_mfma_f32_32x32x2_f32:            4096 */
+#define MB_MFMA_CEILING_OPERAND_BYTES 8192
+int mb_mfma_ceiling(int instruction, const void* operands, float* out, int blocks, int iterations, int warmup,
+                    int launches, void* stream, double* elapsed_s);
+
 /* Description of the last failure on the calling thread ("" if none). */
 const char* mb_last_error(void);
 

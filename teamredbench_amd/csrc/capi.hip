@@ -298,6 +298,26 @@ __global__ void __launch_bounds__(64) clock_stamp_kernel(uint64_t* out) {
 
 }  // namespace
 
+int mb_mfma_ceiling(int instruction, const void* operands, float* out, int blocks, int iterations, int warmup,
+                    int launches, void* stream, double* elapsed_s) {
+    clear_error();
+    if (operands == nullptr || out == nullptr || blocks < 1 || blocks > 65536 || iterations < 1) {
+        set_error("mb_mfma_ceiling: needs operand and output buffers, 1 <= blocks <= 65536, iterations >= 1");
+        return MB_ERR_INVALID_ARG;
+    }
+    if (instruction < MB_MFMA_BF16_32X32X16 || instruction > MB_MFMA_F32_32X32X2) {
+        set_error("mb_mfma_ceiling: unknown instruction %d", instruction);
+        return MB_ERR_INVALID_ARG;
+    }
+    const DeviceProps* props = nullptr;
+    int rc = device_for_launch(&props);
+    if (rc != MB_OK) return rc;
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    const int rounds = (iterations + 1) / 2 * 2;
+    return timed_loop([&]() { return mfma_ceiling_launch(instruction, operands, out, blocks, rounds, st); }, warmup,
+                      launches, st, elapsed_s);
+}
+
 int mb_clock_stamp(uint64_t* out, void* stream) {
     clear_error();
     if (out == nullptr) {

@@ -127,6 +127,9 @@ struct GemmPlan {
 
 int gemm_plan(int dtype, int64_t M, int64_t N, int64_t K, const DeviceProps& props,
               GemmPlan* plan);
+
+// One launch of the MFMA-only kernel of instruction `kind` (MB_MFMA_*).
+int mfma_ceiling_launch(int kind, const void* operands, float* out, int blocks, int iterations, hipStream_t stream);
 int gemm_launch(int dtype, const void* A, const void* B, void* C, int64_t M, int64_t N,
                 int64_t K, float scale_a, float scale_b, void* workspace,
                 const GemmPlan& plan, hipStream_t stream);

@@ -35,6 +35,16 @@ MB_ERR_DEVICE = -5
 NOALLOC_SCRATCH_BYTES = 64 << 20   # MB_NOALLOC_SCRATCH_BYTES
 CLOCK_BLOCKS = 1024                # MB_CLOCK_BLOCKS
 CLOCK_REALTIME_HZ = 100_000_000    # MB_CLOCK_REALTIME_HZ
+# MFMA ceiling instructions (MB_MFMA_*): name -> (code, FLOP per wave instruction, peak-table dtype)
+MFMA_INSTRUCTIONS = {
+    "v_mfma_f32_32x32x16_bf16": (0, 32768, "bfloat16"),
+    "v_mfma_f32_16x16x32_bf16": (1, 16384, "bfloat16"),
+    "v_mfma_scale_f32_32x32x64_f8f6f4": (2, 131072, "float8_e4m3fn"),
+    "v_mfma_scale_f32_16x16x128_f8f6f4": (3, 65536, "float8_e4m3fn"),
+    "v_mfma_f32_32x32x2_f32": (4, 4096, "float32"),
+}
+MFMA_CEILING_OPERAND_BYTES = 8192   # MB_MFMA_CEILING_OPERAND_BYTES
+MFMA_CEILING_CHAINS = 8
 
 OP_COPY, OP_SCALE, OP_TRIAD = 0, 1, 2
 OPS = {"copy": OP_COPY, "scale": OP_SCALE, "triad": OP_TRIAD}
@@ -121,6 +131,11 @@ SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
     ),
     "mb_set_tuning": (ctypes.c_int, [ctypes.c_int, _i64]),
     "mb_clock_stamp": (ctypes.c_int, [_vp, _vp]),
+    "mb_mfma_ceiling": (
+        ctypes.c_int,
+        [ctypes.c_int, _cvp, _vp, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, _vp,
+         ctypes.POINTER(ctypes.c_double)],
+    ),
     "mb_get_tuning": (_i64, [ctypes.c_int]),
 }
 
@@ -226,6 +241,15 @@ class NativeLibrary:
     def clock_stamp(self, out: int, stream: int | None = None) -> None:
         """Enqueue one stamp (4 * CLOCK_BLOCKS uint64 at device address `out`): see mb_clock_stamp."""
         self._check(self.handle.mb_clock_stamp(out, stream or None), "mb_clock_stamp")
+
+    def mfma_ceiling(self, instruction: int, operands: int, out: int, blocks: int, iterations: int, warmup: int,
+                     launches: int, stream: int | None = None) -> float:
+        """Seconds per launch of the MFMA-only kernel (see mb_mfma_ceiling)."""
+        elapsed = ctypes.c_double(0.0)
+        status = self.handle.mb_mfma_ceiling(int(instruction), operands, out, int(blocks), int(iterations), int(warmup),
+                                             int(launches), stream or None, ctypes.byref(elapsed))
+        self._check(status, "mb_mfma_ceiling")
+        return elapsed.value
 
     # ---- plan overrides ----------------------------------------------------
     def set_tuning(self, knob: str, value: int | None) -> None:

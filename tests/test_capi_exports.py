@@ -70,6 +70,13 @@ def test_abi_constants_match_the_header():
     assert shift and int(shift.group(1)) << int(shift.group(2)) == capi.NOALLOC_SCRATCH_BYTES
     assert int(consts["MB_CLOCK_BLOCKS"]) == capi.CLOCK_BLOCKS
     assert int(consts["MB_CLOCK_REALTIME_HZ"]) == capi.CLOCK_REALTIME_HZ
+    assert int(consts["MB_MFMA_CEILING_OPERAND_BYTES"]) == capi.MFMA_CEILING_OPERAND_BYTES
+    codes = {name: code for name, (code, _, _) in capi.MFMA_INSTRUCTIONS.items()}
+    assert codes == {"v_mfma_f32_32x32x16_bf16": int(consts["MB_MFMA_BF16_32X32X16"]),
+                     "v_mfma_f32_16x16x32_bf16": int(consts["MB_MFMA_BF16_16X16X32"]),
+                     "v_mfma_scale_f32_32x32x64_f8f6f4": int(consts["MB_MFMA_FP8_32X32X64"]),
+                     "v_mfma_scale_f32_16x16x128_f8f6f4": int(consts["MB_MFMA_FP8_16X16X128"]),
+                     "v_mfma_f32_32x32x2_f32": int(consts["MB_MFMA_F32_32X32X2"])}
 
 
 def test_tuning_knobs_validate_and_restore_without_a_gpu():
