@@ -1152,7 +1152,15 @@ int gemm_tiled_plan(int dtype, int64_t M, int64_t N, int64_t K, const DeviceProp
     };
     const int forced_cfg = (int)tuning(MB_TUNE_GEMM_TILED_CONFIG);  // -1 unless forced
     const int pinned = forced_cfg >= 0 && n128_only && forced_cfg < 2 ? 2 : forced_cfg;
-    int cfg = pinned >= 0 ? pinned : (!n128_only && tiles(0) >= cus && M % kConfigs[0].bm == 0) ? 0 : -1;
+    // 256 x 256 tiles once they occupy more than half the CUs. Short of a
+    // full round they still beat the smaller tiles, whose twice-as-many
+    // blocks need a second round: on MI355X, 14 shapes with 144 to 240 such
+    // tiles (M 1536..4096, N 3072..8192, K 2048..8192, bf16 and fp8 e4m3) ran
+    // 5-25% faster on them than on the cost model's pick (bf16 3072 x 3072 x
+    // 4096 80.2 against 107.5 us on 128 x 256 tiles at 2 splits, fp8 2560 x
+    // 6144 x 8192 86.2 against 97.6), while at 128 or 64 of them (1024 x 8192,
+    // 2048 x 4096, 2048^2) they ran 27-125% slower.
+    int cfg = pinned >= 0 ? pinned : (!n128_only && 2 * tiles(0) > cus && M % kConfigs[0].bm == 0) ? 0 : -1;
     // Last-round fill. 128 x 256 tiles run 7-14% below 256 x 256 per FLOP on
     // MI355X, and a partly filled last round costs less than a full one (the
     // busy CUs clock up under the power limit), so the smaller tile pays only
@@ -1166,7 +1174,7 @@ int gemm_tiled_plan(int dtype, int64_t M, int64_t N, int64_t K, const DeviceProp
         fill_rule = full <= 2 && rest > 0 && 4 * rest <= cus;
         if (fill_rule) cfg = 1;
     }
-    // Problems with too few 256 x 256 tiles to fill the GPU: the tile
+    // Problems with too few 256 x 256 tiles to fill half the GPU: the tile
     // configuration (128 x 256, 128 x 128 or 64 x 128) and the K split count s
     // (1, 2, 4 .. 32, whole stages per split) that a cost model rates fastest:
     //   blocks  = tiles * s, in ceil(blocks / CUs) rounds;

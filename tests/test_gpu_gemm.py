@@ -639,6 +639,22 @@ def test_mostly_empty_last_round_takes_128_row_tiles(lib, dtype, shape, tile_m):
     assert (info["tile_m"], info["tile_n"], info["split_k"]) == (tile_m, 256, 1)
 
 
+@pytest.mark.parametrize("dtype", ["bfloat16", "float8_e4m3fn"])
+@pytest.mark.parametrize("shape, tile", [((3072, 3072, 4096), (256, 256)), ((1536, 8192, 8192), (256, 256)),
+                                         ((2560, 4096, 8192), (256, 256)), ((3584, 3584, 2048), (256, 256)),
+                                         ((1536, 5632, 512), (256, 256)), ((2048, 4096, 4096), (128, 256)),
+                                         ((1024, 8192, 8192), (128, 256)), ((2048, 2048, 2048), (128, 128))])
+def test_more_than_half_a_round_of_256_row_tiles_takes_them(lib, dtype, shape, tile):
+    # 256 x 256 tiles short of a full round (144 to 240 of them above, 132 for 1536 x 5632) run unsplit in
+    # one round, where 128 x 256 tiles would need two; at 128 or 64 of them the smaller tiles fill the CUs.
+    m, n, k = shape
+    info = lib.gemm_info(capi.DTYPES[dtype], m, n, k)
+    assert (info["tile_m"], info["tile_n"], info["split_k"]) == (*tile, 1), info
+    if k <= 512:
+        print(f"[gemm] partial round {dtype} {shape} -> {tile}", flush=True)
+        _check_random(lib, dtype, m, n, k, seed=m + n, rows=256)
+
+
 def test_overrides_are_reported_and_the_environment_is_ignored(lib, tune, monkeypatch):
     # Plans change only through mb_set_tuning, and kernel_info names every override in force.
     shape = (128, 512, 3 * 64 * 8)
