@@ -1154,12 +1154,14 @@ int gemm_tiled_plan(int dtype, int64_t M, int64_t N, int64_t K, const DeviceProp
     const int pinned = forced_cfg >= 0 && n128_only && forced_cfg < 2 ? 2 : forced_cfg;
     // 256 x 256 tiles once they occupy more than half the CUs. Short of a
     // full round they still beat the smaller tiles, whose twice-as-many
-    // blocks need a second round: on MI355X, 14 shapes with 144 to 240 such
-    // tiles (M 1536..4096, N 3072..8192, K 2048..8192, bf16 and fp8 e4m3) ran
-    // 5-25% faster on them than on the cost model's pick (bf16 3072 x 3072 x
-    // 4096 80.2 against 107.5 us on 128 x 256 tiles at 2 splits, fp8 2560 x
-    // 6144 x 8192 86.2 against 97.6), while at 128 or 64 of them (1024 x 8192,
-    // 2048 x 4096, 2048^2) they ran 27-125% slower.
+    // blocks need a second round: on MI355X, with A and B cycled through
+    // copies that exceed the Infinity Cache, 16 shapes with 132 to 240 such
+    // tiles (M 1536..4096, N 3072..8192, K 512..8192) ran 1.12-1.64x faster on
+    // them than on the cost model's pick, 1.29x in geometric mean over bf16
+    // and fp8 e4m3 (bf16 3072 x 3072 x 4096 74.8 against 104.6 us on 128 x 256
+    // tiles at 2 splits, fp8 4096 x 3072 x 8192 74.5 against 122.4 on 128 x
+    // 128), while at 128 or 64 of them (1024 x 8192, 2048 x 4096, 2048^2) they
+    // ran 27-125% slower.
     int cfg = pinned >= 0 ? pinned : (!n128_only && 2 * tiles(0) > cus && M % kConfigs[0].bm == 0) ? 0 : -1;
     // Last-round fill. 128 x 256 tiles run 7-14% below 256 x 256 per FLOP on
     // MI355X, and a partly filled last round costs less than a full one (the
