@@ -10,12 +10,14 @@ fills the GEMM operands with 0.03125), and reports both figures. The
 comparison is a measurement, not a gate: where the arrays land in HBM moves a
 stream figure by up to ~5% and the part's clock under its power limit moves a
 GEMM figure by as much, so only correctness is asserted here (the constant
-fill's known answer). The figures are written to
-gpurun_out/vs_reference_native.json when that directory exists.
+fill's known answer). Each figure is printed, and the set is written to
+vs_reference_native.json in the directory MI355BENCH_RESULTS_DIR names, when
+that variable is set.
 """
 from __future__ import annotations
 
 import json
+import os
 from pathlib import Path
 import subprocess
 
@@ -45,9 +47,9 @@ def _run_ref(binary: str, args: list[str]) -> float:
 
 def _record(key: str, **values) -> None:
     RESULTS[key] = values
-    out = ROOT / "gpurun_out"
-    if out.is_dir():
-        (out / "vs_reference_native.json").write_text(json.dumps(RESULTS, indent=1), encoding="utf-8")
+    out = os.environ.get("MI355BENCH_RESULTS_DIR")
+    if out and Path(out).is_dir():
+        (Path(out) / "vs_reference_native.json").write_text(json.dumps(RESULTS, indent=1), encoding="utf-8")
     print(f"[vs-reference] {key}: {values}", flush=True)
 
 
