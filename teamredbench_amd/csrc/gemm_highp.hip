@@ -3,11 +3,13 @@
 // accumulated in that type by the MFMAs (fp32: v_mfma_f32_32x32x2_f32; fp64:
 // v_mfma_f64_16x16x4_f64), for any M, N, K >= 1.
 //
-// Two kernels. Shapes made of whole 256 x 256 (fp32) or 256 x 128 (fp64)
-// tiles with at least one tile per CU run on an LDS-DMA ring like the 16-bit
-// pipelined kernel (gemm_f32_dma_kernel, gemm_f64_dma_kernel below: 92% and
-// 88% of peak at 8192^3). Every other shape runs the register-staged kernel
-// that follows, which takes any shape and stays near 80% of peak:
+// Two kernels. Shapes whose A and B rows start on 16 bytes run on an LDS-DMA
+// ring like the 16-bit pipelined kernel (gemm_f32_dma_kernel,
+// gemm_f64_dma_kernel below: 95% and 93% of peak at 8192^3): fp64 on 128 x 128
+// tiles, fp32 on 256 x 256 tiles where their rounds fill the CUs and on
+// 128 x 128 tiles elsewhere (highp_dma_config). Every other shape runs the
+// register-staged kernel that follows, which takes any shape and stays near
+// 80% of peak:
 //
 // Register-staged kernel. Operands come through registers into a
 // double-buffered LDS tile (one barrier per stage), and the next stage's
@@ -30,6 +32,7 @@
 #include "gemm_pipeline.hpp"
 
 #include <cstdlib>
+#include <utility>
 
 namespace mb {
 namespace {
@@ -205,16 +208,16 @@ gemm_highp_kernel(const T* __restrict__ A, const T* __restrict__ B, T* __restric
     }
 }
 
-// ---- fp32 on an LDS-DMA ring (256 x 256 tiles) -----------------------------
+// ---- fp32 on an LDS-DMA ring (256 x 256 and 128 x 128 tiles) ---------------
 //
 // The register-staged kernel above tops out near 80% of the fp32 peak: its
 // load, LDS store and barrier phases leave the matrix pipe idle between MFMA
 // groups. This one follows the 16-bit pipelined kernel instead: A and B go
 // global -> LDS with buffer_load ... lds into a ring of 4 slots (one barrier
 // per stage, loads of stage kt + 3 issued into the slot stage kt - 1 just
-// vacated), and each wave owns 128 x 128 of C as 4 x 4 fragments of
-// v_mfma_f32_32x32x2_f32, so a stage is 128 MFMAs (8192 cycles) against one
-// barrier.
+// vacated), and on 256 x 256 tiles each wave owns 128 x 128 of C as 4 x 4
+// fragments of v_mfma_f32_32x32x2_f32, so a stage is 128 MFMAs (8192 cycles)
+// against one barrier.
 //
 // K order inside a stage. The MFMA sums two K values, one from each lane
 // half; here lane half h supplies K 8h + t at step t (t = 0..7), which is any
@@ -272,16 +275,22 @@ gemm_f32_dma_kernel(const float* __restrict__ A, const float* __restrict__ B, fl
         const int row = lin / BRow, pchunk = (lin % BRow) >> 4;
         b_voff[q] = row * ldb + ((pchunk ^ swz_b32(row)) << 4);
     }
-    auto issue = [&](int kt, int slot) {
+    // DMA instruction q of stage kt into `slot`: A pieces first, then B.
+    // RAGGED_K (K not a multiple of the stage): A pieces at or past K load zeros.
+    auto issue_one = [&](int kt, int slot, auto idx) {
+        constexpr int q = decltype(idx)::value;
         const unsigned base = (unsigned)(uintptr_t)(MB_LDS unsigned char*)ring[slot];
-        // RAGGED_K (K not a multiple of the stage): A pieces at or past K load zeros.
-#pragma unroll
-        for (int q = 0; q < AInstr; ++q)
+        if constexpr (q < AInstr)
             lds_dma16(ra, base + (wave * AInstr + q) * 1024,
                       RAGGED_K && a_kbyte[q] >= K * 4 - kt * 64 ? (int)0x80000000u : a_voff[q], kt * 64);
-#pragma unroll
-        for (int q = 0; q < BInstr; ++q)
-            lds_dma16(rb, base + ABytes + (wave * BInstr + q) * 1024, b_voff[q], kt * kF32StageK * ldb);
+        else
+            lds_dma16(rb, base + ABytes + (wave * BInstr + q - AInstr) * 1024, b_voff[q - AInstr],
+                      kt * kF32StageK * ldb);
+    };
+    auto issue = [&](int kt, int slot) {
+        [&]<int... Q>(std::integer_sequence<int, Q...>) {
+            (issue_one(kt, slot, std::integral_constant<int, Q>{}), ...);
+        }(std::make_integer_sequence<int, Loads>{});
     };
 
     f32x16 acc[FM][FN];
@@ -329,34 +338,47 @@ gemm_f32_dma_kernel(const float* __restrict__ A, const float* __restrict__ B, fl
     };
     // One barrier per stage, at its middle: it certifies that stage kt + 1 has
     // landed for every wave and that every wave is done with stage kt - 1's
-    // slot, which takes stage kt + 3's loads. The next stage's operands are
-    // read under this stage's MFMAs (A's first chunk after the barrier, its
-    // first B operands in the last step, A's second chunk at the boundary), so
-    // a stage boundary has no wait. Past the last stage the loads repeat it (in
-    // bounds, never used).
+    // slot, which takes stage kt + 3's loads. Those loads are spread over the
+    // stage's second half, evenly between its MFMAs (issued back to back after
+    // the barrier, they held the wave's issue for longer than the one MFMA in
+    // flight covers). The next stage's operands are read under this stage's
+    // MFMAs (A's first chunk after the barrier, its first B operands in the
+    // last step, A's second chunk at the boundary), so a stage boundary has no
+    // wait. Past the last stage the loads repeat it (in bounds, never used).
     constexpr int kSteps = kF32StageK / 2, kMid = kSteps / 2;
+    constexpr int kMfma = FM * FN;                               // MFMAs per step
+    constexpr int kLoadSteps = kSteps - kMid;
+    static_assert(Loads % kLoadSteps == 0 && kMfma % (Loads / kLoadSteps) == 0, "loads spread evenly");
+    constexpr int kLoadsPerStep = Loads / kLoadSteps, kLoadGap = kMfma / kLoadsPerStep;
     wait_vmcnt_and_barrier<Loads * (kF32Stages - 2)>();
     read_a(0, 0);
     read_a(0, 1);
     read_b(0, 0, 0);
     for (int kt = 0; kt < ksteps; ++kt) {
-#pragma unroll
-        for (int t = 0; t < kSteps; ++t) {
-            if (t == 0 && kt > 0) read_a(kt, 1);
-            if (t == kMid) {
-                wait_vmcnt_and_barrier<Loads * (kF32Stages - 3)>();
-                issue(min(kt + kF32Stages - 1, last), (kt + kF32Stages - 1) % kF32Stages);
-                read_a(kt + 1, 0);
-            }
-            if (t + 1 < kSteps) read_b(kt, t + 1, (t + 1) & 1);
-            else read_b(kt + 1, 0, 0);
-            __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-            for (int i = 0; i < FM; ++i)
-#pragma unroll
-                for (int j = 0; j < FN; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(b[t & 1][j], a[i][t], acc[i][j], 0, 0, 0);
-        }
+        const int load_kt = min(kt + kF32Stages - 1, last), load_slot = (kt + kF32Stages - 1) % kF32Stages;
+        [&]<int... T>(std::integer_sequence<int, T...>) {
+            ([&] {
+                constexpr int t = T;
+                if (t == 0 && kt > 0) read_a(kt, 1);
+                if constexpr (t == kMid) {
+                    wait_vmcnt_and_barrier<Loads * (kF32Stages - 3)>();
+                    read_a(kt + 1, 0);
+                }
+                if constexpr (t + 1 < kSteps) read_b(kt, t + 1, (t + 1) & 1);
+                else read_b(kt + 1, 0, 0);
+                __builtin_amdgcn_sched_barrier(0);
+                [&]<int... Q>(std::integer_sequence<int, Q...>) {
+                    ([&] {
+                        constexpr int m = Q, i = m / FN, j = m % FN;
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(b[t & 1][j], a[i][t], acc[i][j], 0, 0, 0);
+                        if constexpr (t >= kMid && m % kLoadGap == 0)
+                            issue_one(load_kt, load_slot,
+                                      std::integral_constant<int, (t - kMid) * kLoadsPerStep + m / kLoadGap>{});
+                        __builtin_amdgcn_sched_barrier(0);   // keeps each load where it is placed
+                    }(), ...);
+                }(std::make_integer_sequence<int, kMfma>{});
+            }(), ...);
+        }(std::make_integer_sequence<int, kSteps>{});
     }
     wait_vmcnt_and_barrier<0>();
 
@@ -379,19 +401,24 @@ gemm_f32_dma_kernel(const float* __restrict__ A, const float* __restrict__ B, fl
     }
 }
 
-// ---- fp64 on the same LDS-DMA ring (256 x 128 tiles) -----------------------
+// ---- fp64 on the same LDS-DMA ring (128 x 128 tiles) -----------------------
 //
 // v_mfma_f64_16x16x4_f64 sums four K values, one from each 16-lane group g;
 // here group g supplies K 2g + t at step t (t = 0, 1) of a stage's 8, so a
 // lane's A operands for the stage are 2 consecutive doubles of one row -- one
-// ds_read_b128 per fragment from the [256 rows][64 B] A slot -- and its B
+// ds_read_b128 per fragment from the [128 rows][64 B] A slot -- and its B
 // operand at step t is one double of row 2g + t (ds_read_b64). B keeps its HBM
 // layout, [8 rows][128 doubles = 1024 B]; rows with bit 1 set have their
 // 16-byte chunks XOR 8, so groups 0 and 1 (and 2 and 3), which read rows 2
-// apart (the same banks), land 128 bytes apart. Waves own 128 x 64 of C as
-// 8 x 4 fragments (256 accumulator registers); A is the MFMA's first operand,
+// apart (the same banks), land 128 bytes apart. Waves own 64 x 64 of C as
+// 4 x 4 fragments (64 accumulator registers); A is the MFMA's first operand,
 // so accumulator r of lane l is C row 4r + l / 16, column l % 16, and a store
-// instruction writes 4 rows x 128 bytes straight from registers.
+// instruction writes 4 rows x 128 bytes straight from registers. With 64 KiB
+// of ring and under 200 registers per lane, two blocks fit a CU, one wave of
+// each on every SIMD: on MI355X these tiles ran up to 21% faster than
+// 256 x 128 tiles (one block per CU) on 12 shapes from 3072 x 6144 x 4096 to
+// 10240^2 x 4096, 8192^3 included (73.3 against 72.1 TFLOP/s), and 0.5%
+// slower on one (4608^3).
 constexpr int kF64Stages = 4, kF64StageK = 8;
 
 __device__ __forceinline__ int swz_b64(int row) { return ((row >> 1) & 1) << 3; }
@@ -431,15 +458,20 @@ gemm_f64_dma_kernel(const double* __restrict__ A, const double* __restrict__ B, 
         const int row = lin / BRow, pchunk = (lin % BRow) >> 4;
         b_voff[q] = row * ldb + ((pchunk ^ swz_b64(row)) << 4);
     }
-    auto issue = [&](int kt, int slot) {
+    auto issue_one = [&](int kt, int slot, auto idx) {
+        constexpr int q = decltype(idx)::value;
         const unsigned base = (unsigned)(uintptr_t)(MB_LDS unsigned char*)ring[slot];
-#pragma unroll
-        for (int q = 0; q < AInstr; ++q)
+        if constexpr (q < AInstr)
             lds_dma16(ra, base + (wave * AInstr + q) * 1024,
                       RAGGED_K && a_kbyte[q] >= K * 8 - kt * 64 ? (int)0x80000000u : a_voff[q], kt * 64);
-#pragma unroll
-        for (int q = 0; q < BInstr; ++q)
-            lds_dma16(rb, base + ABytes + (wave * BInstr + q) * 1024, b_voff[q], kt * kF64StageK * ldb);
+        else
+            lds_dma16(rb, base + ABytes + (wave * BInstr + q - AInstr) * 1024, b_voff[q - AInstr],
+                      kt * kF64StageK * ldb);
+    };
+    auto issue = [&](int kt, int slot) {
+        [&]<int... Q>(std::integer_sequence<int, Q...>) {
+            (issue_one(kt, slot, std::integral_constant<int, Q>{}), ...);
+        }(std::make_integer_sequence<int, Loads>{});
     };
 
     f64x4 acc[FM][FN];
@@ -480,26 +512,35 @@ gemm_f64_dma_kernel(const double* __restrict__ A, const double* __restrict__ B, 
     };
     // The fp32 kernel's schedule: one barrier per stage, between its two
     // steps, after which stage kt + 1's A operands are read under the second
-    // step's MFMAs and its first B operands at the end of the stage.
+    // step's MFMAs and its first B operands at the end of the stage; stage
+    // kt + 3's loads are spread evenly between the second step's MFMAs.
+    constexpr int kMfma = FM * FN, kLoadGap = kMfma / Loads;
+    static_assert(kLoadGap >= 1, "a load per MFMA at most");
     auto stage = [&](int kt, auto curc) {
         constexpr int cur = decltype(curc)::value;
-#pragma unroll
-        for (int t = 0; t < 2; ++t) {
-            if (t == 1) {
-                wait_vmcnt_and_barrier<Loads * (kF64Stages - 3)>();
-                issue(min(kt + kF64Stages - 1, last), (kt + kF64Stages - 1) % kF64Stages);
-                read_a(kt + 1, std::integral_constant<int, cur ^ 1>{});
-                read_b(kt + 1, 0, 0);
-            } else {
-                read_b(kt, 1, 1);
-            }
-            __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-            for (int i = 0; i < FM; ++i)
-#pragma unroll
-                for (int j = 0; j < FN; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f64_16x16x4f64(a[cur][i][t], b[t][j], acc[i][j], 0, 0, 0);
-        }
+        const int load_kt = min(kt + kF64Stages - 1, last), load_slot = (kt + kF64Stages - 1) % kF64Stages;
+        [&]<int... T>(std::integer_sequence<int, T...>) {
+            ([&] {
+                constexpr int t = T;
+                if constexpr (t == 1) {
+                    wait_vmcnt_and_barrier<Loads * (kF64Stages - 3)>();
+                    read_a(kt + 1, std::integral_constant<int, cur ^ 1>{});
+                    read_b(kt + 1, 0, 0);
+                } else {
+                    read_b(kt, 1, 1);
+                }
+                __builtin_amdgcn_sched_barrier(0);
+                [&]<int... Q>(std::integer_sequence<int, Q...>) {
+                    ([&] {
+                        constexpr int m = Q, i = m / FN, j = m % FN;
+                        acc[i][j] = __builtin_amdgcn_mfma_f64_16x16x4f64(a[cur][i][t], b[t][j], acc[i][j], 0, 0, 0);
+                        if constexpr (t == 1 && m % kLoadGap == 0 && m / kLoadGap < Loads)
+                            issue_one(load_kt, load_slot, std::integral_constant<int, m / kLoadGap>{});
+                        __builtin_amdgcn_sched_barrier(0);   // keeps each load where it is placed
+                    }(), ...);
+                }(std::make_integer_sequence<int, kMfma>{});
+            }(), ...);
+        }(std::make_integer_sequence<int, 2>{});
     };
     wait_vmcnt_and_barrier<Loads * (kF64Stages - 2)>();
     read_a(0, std::integral_constant<int, 0>{});
@@ -559,21 +600,31 @@ int highp_dma_config(bool f64, int64_t M, int64_t N, int64_t K, int cus, const c
         *why = "M or N >= 2^31 exceeds the 32-bit row and column indexes of the LDS-DMA kernels";
         return 0;
     }
-    const int64_t bm = 256, bn = f64 ? 128 : 256;
     auto tiles = [&](int64_t tm, int64_t tn) { return ((M + tm - 1) / tm) * ((N + tn - 1) / tn); };
-    const bool fits_large = tiles(bm, bn) >= cus && tiles(bm, bn) <= INT32_MAX;
-    if (M % bm == 0 && N % bn == 0 && fits_large) return 1;
-    if (M % 128 == 0 && N % 128 == 0 && tiles(128, 128) <= INT32_MAX) return 2;
-    // Ragged M or N: partial last tiles, the large tile when its tiles cover every CU.
-    if (fits_large) return 1;
-    if (tiles(128, 128) <= INT32_MAX) return 2;
-    *why = "more than 2^31 tiles";
-    return 0;
+    auto rounds = [&](int64_t t) { return (t + cus - 1) / cus; };
+    const int64_t small = tiles(128, 128), large = tiles(256, 256);
+    if (small > INT32_MAX) {
+        *why = "more than 2^31 tiles";
+        return 0;
+    }
+    if (f64) return 2;   // 128 x 128 tiles: two blocks per CU (gemm_f64_dma_kernel)
+    // fp32: 256 x 256 tiles run 2.5% faster per FLOP than 128 x 128 ones
+    // (8192^3, whole rounds of either: 150.1 against 145.8 TFLOP/s on MI355X) but
+    // come in rounds of four times the work, so they are taken only when their
+    // rounds cost no more: rounds(256 x 256) <= rounds(128 x 128) / 4 / 0.975.
+    // This picked the faster tile on all of 12 shapes measured: 256 x 256 at
+    // 4096^3, 8192^3, 6144 x 8192 x 4096 and 5632^2 x 4096 (1.9 rounds, 2%);
+    // 128 x 128 where the last 256 x 256 round is partly empty, 1.05-1.32x
+    // faster there (6144^3 124.5 against 109.5 TFLOP/s, 3072 x 6144 x 4096
+    // 109.3 against 83.9). Ragged M or N: partial last tiles on either.
+    const bool large_pays = large >= cus && 4.0 * 0.975 * (double)rounds(large) <= (double)rounds(small);
+    if (M % 256 == 0 && N % 256 == 0 && large_pays) return 1;
+    if (M % 128 == 0 && N % 128 == 0) return 2;
+    return large_pays ? 1 : 2;
 }
 
-void highp_dma_tile(bool f64, int cfg, int* bm, int* bn) {
-    *bm = cfg == 1 ? 256 : 128;
-    *bn = cfg == 1 ? (f64 ? 128 : 256) : 128;
+void highp_dma_tile(int cfg, int* bm, int* bn) {
+    *bm = *bn = cfg == 1 ? 256 : 128;
 }
 
 template <typename T, int BM, int BN>
@@ -618,7 +669,7 @@ int gemm_highp_plan(int dtype, int64_t M, int64_t N, int64_t K, const DeviceProp
     const int cfg = highp_dma_config(f64, M, N, K, props.cu_count > 0 ? props.cu_count : 256, &why);
     if (cfg != 0) {
         int bm, bn;
-        highp_dma_tile(f64, cfg, &bm, &bn);
+        highp_dma_tile(cfg, &bm, &bn);
         plan->implementation = f64 ? "gfx950_mfma_f64_16x16x4_lds_dma" : "gfx950_mfma_f32_32x32x2_lds_dma";
         plan->threads = 256;
         plan->grid = (int)(((M + bm - 1) / bm) * ((N + bn - 1) / bn));
@@ -672,7 +723,6 @@ int gemm_highp_launch(int dtype, const void* A, const void* B, void* C, int64_t 
             if (plan.config == 2) return launch_dma<float, 128, 128>(A, B, C, M, N, K, stream);
             return launch_typed<float>(A, B, C, M, N, K, stream);
         case MB_DT_FLOAT64:
-            if (plan.config == 1) return launch_dma<double, 256, 128>(A, B, C, M, N, K, stream);
             if (plan.config == 2) return launch_dma<double, 128, 128>(A, B, C, M, N, K, stream);
             return launch_typed<double>(A, B, C, M, N, K, stream);
         default:

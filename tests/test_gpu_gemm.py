@@ -377,14 +377,18 @@ def test_highp_kernel_info(lib, dtype):
 
 
 @pytest.mark.parametrize("shape, tile", [((4096, 4096, 64), (256, 256)), ((8192, 2048, 96), (256, 256)),
-                                         ((4352, 4096, 16), (256, 256)), ((2048, 2048, 2048), (128, 128)),
-                                         ((1024, 1536, 48), (128, 128)), ((4096, 4096, 40), (256, 256)),
-                                         ((4096, 4000, 64), (256, 256)), ((1000, 1000, 64), (128, 128)),
+                                         ((8192, 8192, 64), (256, 256)), ((5632, 5632, 64), (256, 256)),
+                                         ((4352, 4096, 16), (128, 128)), ((6144, 6144, 64), (128, 128)),
+                                         ((2048, 2048, 2048), (128, 128)), ((1024, 1536, 48), (128, 128)),
+                                         ((4096, 4096, 40), (256, 256)), ((4096, 4000, 64), (256, 256)),
+                                         ((1000, 1000, 64), (128, 128)), ((6100, 6100, 64), (128, 128)),
                                          ((4096, 4001, 64), None), ((4096, 4096, 42), None)])
 def test_f32_lds_dma_kernel_selection(lib, shape, tile):
-    # fp32 takes the LDS-DMA ring with 256 x 256 tiles when they cover every CU, else with 128 x 128
-    # tiles when the shape divides (2048^3: 64 large tiles, 256 small), else on partial last tiles; a K
-    # off the 16-deep stage runs whole stages. Rows of A or B off 16 bytes keep the register-staged kernel.
+    # fp32 takes the LDS-DMA ring with 256 x 256 tiles when they cover every CU and their rounds cost
+    # no more than the 128 x 128 tiles' at 0.975 of the rate (4352 x 4096: 2 rounds of 272 large tiles
+    # against 5 of 1088 small; 6144^2: 3 against 9), else 128 x 128 tiles (2048^3: 64 large tiles, 256
+    # small), partial last tiles included; a K off the 16-deep stage runs whole stages. Rows of A or B
+    # off 16 bytes keep the register-staged kernel.
     info = lib.gemm_info(capi.DT_FLOAT32, *shape)
     if tile is None:
         assert info["implementation"] == "gfx950_mfma_f32_32x32x2" and info["tile_m"] == 128
@@ -416,13 +420,14 @@ def test_f32_lds_dma_against_float64_brute_force(lib, shape, tune):
     assert torch.all((staged - ref).abs() <= bound)
 
 
-@pytest.mark.parametrize("shape, tile", [((4096, 8192, 64), (256, 128)), ((8192, 4096, 40), (256, 128)),
+@pytest.mark.parametrize("shape, tile", [((4096, 8192, 64), (128, 128)), ((8192, 4096, 40), (128, 128)),
                                          ((2048, 2048, 2048), (128, 128)), ((1024, 1536, 40), (128, 128)),
-                                         ((4096, 8192, 60), (256, 128)), ((4096, 8000, 64), (256, 128)),
+                                         ((4096, 8192, 60), (128, 128)), ((4096, 8000, 64), (128, 128)),
+                                         ((8192, 8192, 64), (128, 128)),
                                          ((4096, 8001, 64), None), ((4096, 8192, 61), None)])
 def test_f64_lds_dma_kernel_selection(lib, shape, tile):
-    # fp64: 256 x 128 tiles when they cover every CU, else 128 x 128, partial last tiles and a K off the
-    # 8-deep stage included; rows of A or B off 16 bytes keep the register-staged kernel.
+    # fp64: 128 x 128 tiles for every shape the ring takes (two blocks per CU), partial last tiles and a
+    # K off the 8-deep stage included; rows of A or B off 16 bytes keep the register-staged kernel.
     info = lib.gemm_info(capi.DT_FLOAT64, *shape)
     if tile is None:
         assert info["implementation"] == "gfx950_mfma_f64_16x16x4" and info["tile_m"] == 128
