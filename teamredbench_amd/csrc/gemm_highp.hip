@@ -566,11 +566,10 @@ gemm_f64_dma_kernel(const double* __restrict__ A, const double* __restrict__ B, 
         }
 }
 
-// Which LDS-DMA ring a shape takes: 1 = the large tile (fp32 256 x 256, fp64
-// 256 x 128) when its tiles cover every CU, 2 = 128 x 128 when the shape
-// divides into it (2048^3 makes 64 large tiles but 256 small ones); a shape
-// that divides into neither takes partial last tiles, on the large tile when
-// those cover every CU. 0 = the register-staged kernel, with *why naming the
+// Which LDS-DMA ring a shape takes: 1 = fp32 on 256 x 256 tiles, when they
+// cover every CU and their rounds cost no more than 128 x 128 tiles' (rule
+// below); 2 = 128 x 128 tiles, every other fp32 shape and every fp64 one,
+// partial last tiles included. 0 = the register-staged kernel, with *why naming the
 // reason: A's or B's rows not on 16 bytes, or buffer offsets (B's K x N bytes,
 // a 256-row A panel) beyond 31 bits. A K that is not whole stages runs the
 // RAGGED_K instantiations, whose A pieces past K load zeros.
