@@ -399,7 +399,7 @@ def test_f32_lds_dma_kernel_selection(lib, shape, tile):
 
 
 @pytest.mark.parametrize("shape", [(4096, 4096, 64), (8192, 2048, 96), (1024, 1536, 48), (2048, 2048, 16),
-                                   (1000, 1000, 1000), (300, 1012, 60), (2100, 900, 36)])
+                                   (4352, 4096, 16), (1000, 1000, 1000), (300, 1012, 60), (2100, 900, 36)])
 def test_f32_lds_dma_against_float64_brute_force(lib, shape, tune):
     # The LDS-DMA kernel sums each stage's 16 K values in a permuted order (lane half h takes K 8h + t
     # at step t); every element must still sit within the fp32 accumulation bound of an fp64
