@@ -597,7 +597,8 @@ gemm_tiled_kernel(const unsigned char* __restrict__ A, const unsigned char* __re
     // from registers, every store instruction would put 16 bytes into each of
     // 32 rows. Instead each wave rounds its (WTM x WTN) tile to 16 bits into
     // its own region of the LDS ring (all of it is free after the final wait
-    // and barrier), then reads it back row by row so that 16 (8, 4) lanes
+    // and barrier), 32 rows at a time for 128-row wave tiles, and reads them
+    // back row by row so that 16 (8, 4) lanes
     // store one 256-byte (128-, 64-byte) row segment of a 128- (64-, 32-)
     // column wave tile: whole cache lines (half lines for 32 columns), half
     // the store instructions. Staged rows are 16 (8, 4) chunks of 16 bytes;
@@ -619,31 +620,42 @@ gemm_tiled_kernel(const unsigned char* __restrict__ A, const unsigned char* __re
         static_assert(W * WTM * ROW_BYTES <= LDS_BYTES, "the waves' tiles must fit the LDS ring");
         unsigned char* stage = lds + wave * WTM * ROW_BYTES;
         // alpha is 1 except for scaled fp8: the unscaled instantiation skips
-        // the multiply, a VALU op per accumulator.
-        auto stage_tile = [&](auto scaled) {
+        // the multiply, a VALU op per accumulator. Waves of 128 rows stage and
+        // store 32 rows at a time, so a group's stores go out while the next
+        // group is rounded; shorter wave tiles in one group (smaller groups
+        // shorten their read-back batches, which cost 2-4% there).
+        constexpr int GROUP = WTM >= 128 ? 32 : WTM;          // C rows per staged group
+        auto stage_row = [&](auto irow) {
+            constexpr int i = decltype(irow)::value;
+            const int r = 32 * i + (lane & 31);
 #pragma unroll
-            for (int i = 0; i < FM; ++i) {
-                const int r = 32 * i + (lane & 31);
+            for (int j = 0; j < FN; ++j) {
 #pragma unroll
-                for (int j = 0; j < FN; ++j) {
-#pragma unroll
-                    for (int g = 0; g < 4; ++g) {
-                        const f32x16& v = acc[i][j];
-                        u32x2 packed;
-                        if constexpr (decltype(scaled)::value) {
-                            packed = pack4<DT>(v[4 * g] * alpha, v[4 * g + 1] * alpha, v[4 * g + 2] * alpha,
-                                               v[4 * g + 3] * alpha);
-                        } else {
-                            packed = pack4<DT>(v[4 * g], v[4 * g + 1], v[4 * g + 2], v[4 * g + 3]);
-                        }
-                        const int chunk = (4 * j + g) ^ (r % ROW_CHUNKS);
-                        *reinterpret_cast<u32x2*>(stage + r * ROW_BYTES + chunk * 16 + 8 * half) = packed;
+                for (int g = 0; g < 4; ++g) {
+                    const f32x16& v = acc[i][j];
+                    u32x2 packed;
+                    if constexpr (SCALED) {
+                        packed = pack4<DT>(v[4 * g] * alpha, v[4 * g + 1] * alpha, v[4 * g + 2] * alpha,
+                                           v[4 * g + 3] * alpha);
+                    } else {
+                        packed = pack4<DT>(v[4 * g], v[4 * g + 1], v[4 * g + 2], v[4 * g + 3]);
                     }
+                    const int chunk = (4 * j + g) ^ (r % ROW_CHUNKS);
+                    *reinterpret_cast<u32x2*>(stage + r * ROW_BYTES + chunk * 16 + 8 * half) = packed;
                 }
             }
         };
-        stage_tile(std::integral_constant<bool, SCALED>{});
-        store_staged_tile<WTM, ROW_BYTES>(stage, C, M, N, tm * BM + wm * WTM, (int64_t)tn * BN + wn * WTN, lane);
+        // Groups start on multiples of 32 rows, which keeps the staging swizzle (row % ROW_CHUNKS, ROW_CHUNKS <= 16).
+        [&]<int... G>(std::integer_sequence<int, G...>) {
+            ([&] {
+                constexpr int grp = G;
+                [&]<int... I>(std::integer_sequence<int, I...>) {
+                    (stage_row(std::integral_constant<int, grp * (GROUP / 32) + I>{}), ...);
+                }(std::make_integer_sequence<int, GROUP / 32>{});
+                store_staged_tile<GROUP, ROW_BYTES>(stage + GROUP * grp * ROW_BYTES, C, M, N,
+                                                    tm * BM + wm * WTM + GROUP * grp, (int64_t)tn * BN + wn * WTN, lane);
+            }(), ...);
+        }(std::make_integer_sequence<int, WTM / GROUP>{});
     } else if constexpr (BM <= 128) {
         float* part = ws + (int64_t)split * M * N;
 #pragma unroll
@@ -972,20 +984,32 @@ gemm_fp8_mi16_kernel(const unsigned char* __restrict__ A, const unsigned char* _
         static_assert(ROW_CHUNKS == 16 || ROW_CHUNKS == 8, "staging covers wave tiles 128 or 64 columns wide");
         static_assert(W * WTM * ROW_BYTES <= LDS_BYTES, "the waves' tiles must fit the LDS ring");
         unsigned char* stage = lds + wave * WTM * ROW_BYTES;
+        // Waves of 128 rows in groups of 32 (two fragment rows), as in
+        // gemm_tiled_kernel: a group's stores go out while the next is
+        // rounded; groups start on multiples of 32 rows, which keeps the
+        // staging swizzle. Shorter wave tiles in one group.
+        constexpr int GROUP = WTM >= 128 ? 32 : WTM;          // C rows per staged group
+        static_assert(GROUP % 16 == 0 && WTM % GROUP == 0, "groups of whole fragment rows");
+        [&]<int... P>(std::integer_sequence<int, P...>) {
+            ([&] {
+                constexpr int p = P;
 #pragma unroll
-        for (int i = 0; i < FM; ++i) {
-            const int r = 16 * i + l16;
+                for (int i = p * (GROUP / 16); i < (p + 1) * (GROUP / 16); ++i) {
+                    const int r = 16 * i + l16;
 #pragma unroll
-            for (int j = 0; j < FN; ++j) {
-                const f32x4& v = acc[i][j];
-                u32x2 packed;
-                if constexpr (SCALED) packed = pack4<DT>(v[0] * alpha, v[1] * alpha, v[2] * alpha, v[3] * alpha);
-                else packed = pack4<DT>(v[0], v[1], v[2], v[3]);
-                const int chunk = (2 * j + (g >> 1)) ^ (r % ROW_CHUNKS);
-                *reinterpret_cast<u32x2*>(stage + r * ROW_BYTES + chunk * 16 + 8 * (g & 1)) = packed;
-            }
-        }
-        store_staged_tile<WTM, ROW_BYTES>(stage, C, M, N, tm * BM + wm * WTM, (int64_t)tn * BN + wn * WTN, lane);
+                    for (int j = 0; j < FN; ++j) {
+                        const f32x4& v = acc[i][j];
+                        u32x2 packed;
+                        if constexpr (SCALED) packed = pack4<DT>(v[0] * alpha, v[1] * alpha, v[2] * alpha, v[3] * alpha);
+                        else packed = pack4<DT>(v[0], v[1], v[2], v[3]);
+                        const int chunk = (2 * j + (g >> 1)) ^ (r % ROW_CHUNKS);
+                        *reinterpret_cast<u32x2*>(stage + r * ROW_BYTES + chunk * 16 + 8 * (g & 1)) = packed;
+                    }
+                }
+                store_staged_tile<GROUP, ROW_BYTES>(stage + GROUP * p * ROW_BYTES, C, M, N, tm * BM + wm * WTM + GROUP * p,
+                                                    (int64_t)tn * BN + wn * WTN, lane);
+            }(), ...);
+        }(std::make_integer_sequence<int, WTM / GROUP>{});
     } else if constexpr (BM <= 128) {
         float* part = ws + (int64_t)split * M * N;
         const int row0 = tm * BM + wm * WTM + l16;
