@@ -312,7 +312,7 @@ gemm_f32_dma_kernel(const float* __restrict__ A, const float* __restrict__ B, fl
     // mid-stage barrier) and its second chunk at the stage boundary, four
     // steps before it is needed: one register set.
     float a[FM][8];
-    float b[2][FN];     // B operands of this step and the next
+    float b[4][FN];     // B operands of steps t .. t + 3, read two steps ahead
     auto read_a = [&](int kt, int e) {
         const unsigned char* slot = ring[kt % kF32Stages];
 #pragma unroll
@@ -342,10 +342,15 @@ gemm_f32_dma_kernel(const float* __restrict__ A, const float* __restrict__ B, fl
     // stage's second half, evenly between its MFMAs (issued back to back after
     // the barrier, they held the wave's issue for longer than the one MFMA in
     // flight covers). The next stage's operands are read under this stage's
-    // MFMAs (A's first chunk after the barrier, its first B operands in the
-    // last step, A's second chunk at the boundary), so a stage boundary has no
-    // wait. Past the last stage the loads repeat it (in bounds, never used).
+    // MFMAs (A's first chunk after the barrier, its first two B operands in
+    // the last two steps, A's second chunk at the boundary), so a stage
+    // boundary has no wait. B is read two steps (8 or 32 MFMAs) ahead of its
+    // use: on 128 x 128 tiles one step (4 MFMAs) did not cover the LDS
+    // latency when two blocks share a CU (3072 x 6144 x 4096 ran 17% faster
+    // with two; other shapes within 0.7%). Past the last stage the loads
+    // repeat it (in bounds, never used).
     constexpr int kSteps = kF32StageK / 2, kMid = kSteps / 2;
+    static_assert(kSteps % 4 == 0 && kMid >= 2, "B sets cycle with the stage; next-stage reads follow the barrier");
     constexpr int kMfma = FM * FN;                               // MFMAs per step
     constexpr int kLoadSteps = kSteps - kMid;
     static_assert(Loads % kLoadSteps == 0 && kMfma % (Loads / kLoadSteps) == 0, "loads spread evenly");
@@ -354,6 +359,7 @@ gemm_f32_dma_kernel(const float* __restrict__ A, const float* __restrict__ B, fl
     read_a(0, 0);
     read_a(0, 1);
     read_b(0, 0, 0);
+    read_b(0, 1, 1);
     for (int kt = 0; kt < ksteps; ++kt) {
         const int load_kt = min(kt + kF32Stages - 1, last), load_slot = (kt + kF32Stages - 1) % kF32Stages;
         [&]<int... T>(std::integer_sequence<int, T...>) {
@@ -364,13 +370,14 @@ gemm_f32_dma_kernel(const float* __restrict__ A, const float* __restrict__ B, fl
                     wait_vmcnt_and_barrier<Loads * (kF32Stages - 3)>();
                     read_a(kt + 1, 0);
                 }
-                if constexpr (t + 1 < kSteps) read_b(kt, t + 1, (t + 1) & 1);
-                else read_b(kt + 1, 0, 0);
+                // (t + 2) & 3 is also the set of step t + 2 - kSteps of the next stage: kSteps % 4 == 0
+                if constexpr (t + 2 < kSteps) read_b(kt, t + 2, (t + 2) & 3);
+                else read_b(kt + 1, t + 2 - kSteps, (t + 2) & 3);
                 __builtin_amdgcn_sched_barrier(0);
                 [&]<int... Q>(std::integer_sequence<int, Q...>) {
                     ([&] {
                         constexpr int m = Q, i = m / FN, j = m % FN;
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(b[t & 1][j], a[i][t], acc[i][j], 0, 0, 0);
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(b[t & 3][j], a[i][t], acc[i][j], 0, 0, 0);
                         if constexpr (t >= kMid && m % kLoadGap == 0)
                             issue_one(load_kt, load_slot,
                                       std::integral_constant<int, (t - kMid) * kLoadsPerStep + m / kLoadGap>{});
